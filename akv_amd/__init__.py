@@ -1,0 +1,18 @@
+"""akv_amd: MI355X-native (gfx950) Drop + Reposition of retained KV.
+
+A drop-in for the KV-cache hot path of thu-nics/AKV:
+
+* ``akv_amd.ops.reposition_kv_layers`` -- fused all-layer K re-rotation and
+  K-tail / V move (HIP kernel, bit-exact with the reference arithmetic);
+* ``akv_amd.tables.compact_rows`` -- batched page-table compaction: terminal
+  request rows, freed slots, copy lists, decode layout and compacted rows;
+* ``akv_amd.page_table`` -- decode indices, window lengths, indptr rebuild,
+  side-row scatter and the ``ContextDecodeRegistry`` / ``ContextDecodeLayout``
+  interfaces;
+* ``akv_amd.plan.compile_context_layout`` -- the host event compiler.
+
+All device work is in ``libakv_amd.so`` (C ABI: ``include/akv_amd.h``),
+built by ``python -m akv_amd.build``.  There is no CPU fallback.
+"""
+
+__version__ = "0.1.0"

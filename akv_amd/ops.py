@@ -1,0 +1,274 @@
+"""Drop-in ``reposition_kv_layers`` on the gfx950 HIP kernel.
+
+Same signature, argument meaning, validation order and ``ValueError``
+messages as the reference wrapper
+(``akv/system/sglang/kernels/ops/attention/context_reposition.py:126-236``);
+the launch goes to ``akv_reposition_kv_layers`` in ``libakv_amd.so`` on the
+current HIP stream of the KV device.  No allocation, no device-to-host read,
+no synchronisation.
+"""
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+_KV_DTYPES = {torch.float32: _lib.AKV_F32, torch.float16: _lib.AKV_F16, torch.bfloat16: _lib.AKV_BF16}
+
+
+def current_stream_handle(device):
+    """hipStream_t of torch's current stream on ``device``, as an int."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class _on_device:
+    """Makes ``device`` current for the duration of a launch (cheap when it already is)."""
+
+    __slots__ = ("index", "previous")
+
+    def __init__(self, device):
+        self.index = device.index if device.index is not None else torch.cuda.current_device()
+        self.previous = None
+
+    def __enter__(self):
+        current = torch.cuda.current_device()
+        if current != self.index:
+            self.previous = current
+            torch.cuda.set_device(self.index)
+        return self
+
+    def __exit__(self, *exc):
+        if self.previous is not None:
+            torch.cuda.set_device(self.previous)
+        return False
+
+
+def reposition_kv_layers(
+    k_data_ptrs: torch.Tensor,
+    v_data_ptrs: torch.Tensor,
+    k_layout: torch.Tensor,
+    v_layout: torch.Tensor,
+    source_slots: torch.Tensor,
+    destination_slots: torch.Tensor,
+    position_pairs: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    *,
+    is_neox_style: bool = True,
+    page_size: int = 1,
+    skip_unmapped: bool = False,
+    rotary_dim: int | None = None,
+) -> None:
+    """Rotate K and copy V across native per-layer pools in one GPU launch.
+
+    ``k_data_ptrs``/``v_data_ptrs`` are device tables of per-layer base
+    addresses; every layer shares the exemplar ``k_layout``/``v_layout``
+    dtype and NHD strides.  For each moved token, K's rotary part goes from
+    ``position_pairs[t, 0]`` to ``position_pairs[t, 1]`` and K's tail and V
+    are copied, from ``source_slots[t]`` to ``destination_slots[t]``.
+
+    The caller owns fresh destination slots disjoint from all sources and
+    keeps the sources and metadata alive until the stream finishes.  This
+    wrapper does no GPU-to-CPU read and no synchronisation, and allocates no
+    KV page.
+    """
+    if page_size != 1:
+        raise ValueError("Context Reposition requires page_size=1")
+    tensors = (
+        k_data_ptrs,
+        v_data_ptrs,
+        k_layout,
+        v_layout,
+        source_slots,
+        destination_slots,
+        position_pairs,
+        cos_sin_cache,
+    )
+    if not k_layout.is_cuda or any(t.device != k_layout.device for t in tensors):
+        raise ValueError("Reposition tensors must be on one CUDA device")
+    if k_layout.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError("Context Reposition requires unquantized floating-point KV")
+    if (
+        k_layout.ndim != 3
+        or v_layout.shape != k_layout.shape
+        or v_layout.dtype != k_layout.dtype
+    ):
+        raise ValueError("Reposition requires matching native NHD K/V layouts")
+    if k_layout.stride(-1) != 1 or v_layout.stride(-1) != 1:
+        raise ValueError("Reposition requires contiguous head dimensions")
+    if (
+        k_data_ptrs.ndim != 1
+        or v_data_ptrs.shape != k_data_ptrs.shape
+        or k_data_ptrs.dtype not in (torch.uint64, torch.int64)
+        or v_data_ptrs.dtype not in (torch.uint64, torch.int64)
+        or not k_data_ptrs.is_contiguous()
+        or not v_data_ptrs.is_contiguous()
+    ):
+        raise ValueError("Reposition requires contiguous 64-bit layer pointer tables")
+    count = len(source_slots)
+    if (
+        source_slots.ndim != 1
+        or destination_slots.shape != source_slots.shape
+        or source_slots.dtype != torch.int32
+        or destination_slots.dtype != torch.int32
+        or not source_slots.is_contiguous()
+        or not destination_slots.is_contiguous()
+        or position_pairs.shape != (count, 2)
+        or position_pairs.dtype != torch.int32
+        or position_pairs.stride(-1) != 1
+    ):
+        raise ValueError("Reposition requires int32 slot vectors and [N, 2] positions")
+    head_dim = k_layout.shape[-1]
+    rotary_dim = head_dim if rotary_dim is None else rotary_dim
+    if (
+        type(rotary_dim) is not int
+        or not 0 < rotary_dim <= head_dim
+        or rotary_dim % 2
+        or cos_sin_cache.ndim != 2
+        or cos_sin_cache.shape[1] != rotary_dim
+        or cos_sin_cache.stride(-1) != 1
+        or not cos_sin_cache.is_floating_point()
+    ):
+        raise ValueError("Reposition requires a native cos/sin cache matching rotary_dim")
+    if count == 0 or len(k_data_ptrs) == 0:
+        return
+    table_dtype = _KV_DTYPES.get(cos_sin_cache.dtype)
+    if table_dtype is None:
+        raise ValueError("Reposition cos/sin cache must be float32, float16 or bfloat16")
+    lib = _lib.load()
+    with _on_device(k_layout.device):
+        rc = lib.akv_reposition_kv_layers(
+            k_data_ptrs.data_ptr(),
+            v_data_ptrs.data_ptr(),
+            len(k_data_ptrs),
+            _KV_DTYPES[k_layout.dtype],
+            k_layout.shape[1],
+            head_dim,
+            rotary_dim,
+            k_layout.stride(0),
+            k_layout.stride(1),
+            v_layout.stride(0),
+            v_layout.stride(1),
+            source_slots.data_ptr(),
+            destination_slots.data_ptr(),
+            position_pairs.data_ptr(),
+            position_pairs.stride(0),
+            count,
+            cos_sin_cache.data_ptr(),
+            table_dtype,
+            cos_sin_cache.stride(0),
+            1 if is_neox_style else 0,
+            1 if skip_unmapped else 0,
+            current_stream_handle(k_layout.device),
+        )
+    _lib.check(rc, "akv_reposition_kv_layers")
+
+
+@dataclass(frozen=True)
+class ContextLayerCopy:
+    """One layer's fresh destinations, bound before model execution.
+
+    Mirrors ``ContextLayerCopy``
+    (``akv/system/sglang/srt/layers/attention/context_backend.py:302-341``):
+    ``apply`` runs the single-layer Reposition of this forward's copies.
+    """
+
+    k_data_ptrs: torch.Tensor
+    v_data_ptrs: torch.Tensor
+    k_layout: torch.Tensor
+    v_layout: torch.Tensor
+    source_slots: torch.Tensor
+    destination_slots: torch.Tensor
+    position_pairs: torch.Tensor
+    cos_sin_cache: torch.Tensor
+    is_neox_style: bool
+    skip_unmapped: bool = False
+    rotary_dim: int | None = None
+
+    def apply(self):
+        if len(self.k_data_ptrs) != 1 or len(self.v_data_ptrs) != 1:
+            raise ValueError("Per-layer birth copies must address exactly one layer")
+        reposition_kv_layers(
+            self.k_data_ptrs,
+            self.v_data_ptrs,
+            self.k_layout,
+            self.v_layout,
+            self.source_slots,
+            self.destination_slots,
+            self.position_pairs,
+            self.cos_sin_cache,
+            is_neox_style=self.is_neox_style,
+            skip_unmapped=self.skip_unmapped,
+            rotary_dim=self.rotary_dim,
+        )
+
+
+@dataclass(frozen=True)
+class PoolLayer:
+    """One attention layer's KV buffers and RoPE binding (``ContextPoolLayer``)."""
+
+    layer_id: int
+    sliding_window: bool
+    k_buffer: torch.Tensor
+    v_buffer: torch.Tensor
+    cos_sin_cache: torch.Tensor
+    is_neox_style: bool
+    rotary_dim: int
+
+
+class LayerGroups:
+    """Groups compatible layers so one launch repositions all of them.
+
+    Mirrors ``ContextModelBinding.reposition_existing``
+    (``akv/system/sglang/srt/layers/attention/context_backend.py:432-472``):
+    layers that share (window kind, shape, strides, dtype, RoPE table, style,
+    rotary width) go into one pointer table, built once on the device.
+    ``swa_translate`` maps full-attention slots to a separate SWA pool's slots
+    (``None`` when SWA layers share the full pool).
+    """
+
+    def __init__(self, layers):
+        groups = {}
+        for layer in layers:
+            key = (
+                layer.sliding_window,
+                tuple(layer.k_buffer.shape),
+                layer.k_buffer.stride(),
+                layer.v_buffer.stride(),
+                layer.k_buffer.dtype,
+                layer.cos_sin_cache.data_ptr(),
+                layer.is_neox_style,
+                layer.rotary_dim,
+            )
+            groups.setdefault(key, []).append(layer)
+        self.groups = []
+        for items in groups.values():
+            device = items[0].k_buffer.device
+            k_ptrs = torch.tensor([x.k_buffer.data_ptr() for x in items], dtype=torch.uint64).to(device)
+            v_ptrs = torch.tensor([x.v_buffer.data_ptr() for x in items], dtype=torch.uint64).to(device)
+            self.groups.append((items[0], k_ptrs, v_ptrs))
+
+    @property
+    def launches(self):
+        return len(self.groups)
+
+    def reposition_existing(self, source, destination, positions, swa_translate=None):
+        for layer, k_ptrs, v_ptrs in self.groups:
+            src, dst, separate_swa = source, destination, False
+            if layer.sliding_window and swa_translate is not None:
+                separate_swa = True
+                src = swa_translate(source).to(torch.int32)
+                dst = swa_translate(destination).to(torch.int32)
+            reposition_kv_layers(
+                k_ptrs,
+                v_ptrs,
+                layer.k_buffer,
+                layer.v_buffer,
+                src,
+                dst,
+                positions,
+                layer.cos_sin_cache,
+                is_neox_style=layer.is_neox_style,
+                rotary_dim=layer.rotary_dim,
+                skip_unmapped=separate_swa,
+            )

@@ -1,0 +1,203 @@
+"""Batched page-table compaction after Drop + Reposition (host side).
+
+The device work runs in ``akv_compact_rows`` (``libakv_amd.so``).  This
+module packs the CPU-known per-request metadata (keep mask, birth and final
+positions -- all from the compiled layout) into one host-to-device copy, like
+the reference's packed transfers (``occurrence.py:721-736``), allocates the
+outputs whose sizes the CPU layout already fixes, and launches.
+
+Semantics per request (single-owner final forward, ``occurrence.py:632-767``):
+
+* raw row, in place:  ``keep ? (moved ? fresh : birth) : -1`` (``terminal_slots``);
+* retired:            birth slots of dropped or moved tokens, raw order;
+* copies:             ``(birth slot, fresh slot, (birth pos, final pos))`` of
+                      moved tokens -- exactly the Reposition inputs;
+* decode layout:      ``raw_indices = flatnonzero(keep)`` and their positions
+                      (``ContextDecodeLayout.from_layout``, ``occurrence.py:47-66``);
+* ``kv_indices``:     the compacted row, then ``generated`` raw entries after the
+                      prompt (``request_active_slots``, ``context_transfer.py:110-128``),
+                      laid out by ``kv_indptr``.
+"""
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from .ops import _on_device, current_stream_handle
+
+
+@dataclass
+class CompactionInputs:
+    """Device copies of the per-token metadata of a batch (request-major)."""
+
+    req_offsets: torch.Tensor  # int64 [B+1]
+    keep: torch.Tensor  # uint8 [N]
+    birth_positions: torch.Tensor  # int32 [N]
+    final_positions: torch.Tensor  # int32 [N]
+    n_tokens: tuple
+    kept: tuple
+    moved: tuple
+    max_tokens: int
+
+    @property
+    def n_requests(self):
+        return len(self.n_tokens)
+
+    @property
+    def kept_total(self):
+        return sum(self.kept)
+
+    @property
+    def moved_total(self):
+        return sum(self.moved)
+
+    @property
+    def retired_total(self):
+        return sum(n - k + m for n, k, m in zip(self.n_tokens, self.kept, self.moved))
+
+
+def pack_compaction_inputs(layouts, device):
+    """One host-to-device copy of every request's keep / birth / final arrays.
+
+    ``layouts``: objects with CPU ``keep_mask``, ``birth_positions`` and
+    ``positions`` (a ``ContextLayout``).
+    """
+    keeps, births, finals, ns, kept, moved = [], [], [], [], [], []
+    for layout in layouts:
+        keep = np.asarray(layout.keep_mask, dtype=bool)
+        birth = np.asarray(layout.birth_positions, dtype=np.int32)
+        final = np.asarray(layout.positions, dtype=np.int32)
+        keeps.append(keep)
+        births.append(birth)
+        finals.append(final)
+        ns.append(len(keep))
+        kept.append(int(keep.sum()))
+        moved.append(int((keep & (birth != final)).sum()))
+    total = sum(ns)
+    offsets = np.zeros(len(ns) + 1, dtype=np.int64)
+    offsets[1:] = np.cumsum(ns)
+    # int32 words: birth | final | offsets (as 2 words each) | keep (bytes, padded)
+    keep_words = (total + 3) // 4
+    packed = np.zeros(2 * total + 2 * len(offsets) + keep_words, dtype=np.int32)
+    packed[:total] = np.concatenate(births) if total else []
+    packed[total : 2 * total] = np.concatenate(finals) if total else []
+    packed[2 * total : 2 * total + 2 * len(offsets)] = offsets.view(np.int32)
+    keep_bytes = packed[2 * total + 2 * len(offsets) :].view(np.uint8)
+    if total:
+        keep_bytes[:total] = np.concatenate(keeps).astype(np.uint8)
+    host = torch.from_numpy(packed).pin_memory() if torch.cuda.is_available() else torch.from_numpy(packed)
+    dev = host.to(device, non_blocking=True)
+    off = 2 * total
+    return CompactionInputs(
+        req_offsets=dev[off : off + 2 * len(offsets)].view(torch.int64),
+        keep=dev[off + 2 * len(offsets) :].view(torch.uint8)[:total],
+        birth_positions=dev[:total],
+        final_positions=dev[total : 2 * total],
+        n_tokens=tuple(ns),
+        kept=tuple(kept),
+        moved=tuple(moved),
+        max_tokens=max(ns) if ns else 0,
+    )
+
+
+@dataclass
+class CompactionOutputs:
+    retired: torch.Tensor
+    copy_src: torch.Tensor
+    copy_dst: torch.Tensor
+    copy_pairs: torch.Tensor
+    raw_indices: torch.Tensor
+    active_positions: torch.Tensor
+    kv_indices: torch.Tensor | None
+    kv_indptr: torch.Tensor | None
+    counts: torch.Tensor
+    status: torch.Tensor
+    workspace: torch.Tensor
+
+
+def allocate_outputs(inputs, device, *, generated_total=None):
+    """Outputs of exactly the sizes the CPU layouts fix (no device read-back)."""
+    lib = _lib.load()
+    i32 = torch.int32
+    ws_bytes = lib.akv_compact_workspace_bytes(inputs.n_requests, inputs.max_tokens)
+    kv = None
+    indptr = None
+    if generated_total is not None:
+        kv = torch.empty(inputs.kept_total + generated_total, dtype=i32, device=device)
+        indptr = torch.empty(inputs.n_requests + 1, dtype=i32, device=device)
+    return CompactionOutputs(
+        retired=torch.empty(inputs.retired_total, dtype=i32, device=device),
+        copy_src=torch.empty(inputs.moved_total, dtype=i32, device=device),
+        copy_dst=torch.empty(inputs.moved_total, dtype=i32, device=device),
+        copy_pairs=torch.empty((inputs.moved_total, 2), dtype=i32, device=device),
+        raw_indices=torch.empty(inputs.kept_total, dtype=i32, device=device),
+        active_positions=torch.empty(inputs.kept_total, dtype=i32, device=device),
+        kv_indices=kv,
+        kv_indptr=indptr,
+        counts=torch.empty((inputs.n_requests, 3), dtype=i32, device=device),
+        status=torch.zeros(1, dtype=i32, device=device),
+        workspace=torch.empty(max(8, (ws_bytes + 7) // 8), dtype=torch.int64, device=device),
+    )
+
+
+def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_pointers=None,
+                 generated=None):
+    """Rewrite each request's raw row to its terminal form and emit the lists.
+
+    ``req_to_token``: int32 ``[pool_rows, width]`` request table (rows hold the
+    birth slots on entry).  ``req_rows``: int64 ``[B]`` pool row per request.
+    ``fresh_slots``: int32 ``[M]`` fresh slots, request-major raw order of the
+    moved tokens.  ``row_pointers``: optional int64 ``[pool_rows]`` side-row
+    table (``RowPointers``, ``akv/system/sglang.patch:242-278``).  ``generated``:
+    optional int32 ``[B]`` count of generated entries to append per request.
+    """
+    if req_to_token.dtype != torch.int32 or req_to_token.ndim != 2 or req_to_token.stride(1) != 1:
+        raise ValueError("req_to_token must be an int32 [rows, width] table with unit column stride")
+    if req_rows.dtype != torch.int64 or req_rows.shape != (inputs.n_requests,):
+        raise ValueError("req_rows must be int64 [B]")
+    if fresh_slots.dtype != torch.int32 or fresh_slots.shape != (inputs.moved_total,):
+        raise ValueError("fresh_slots must be int32 with one slot per moved token")
+    if row_pointers is not None and row_pointers.dtype != torch.int64:
+        raise ValueError("row_pointers must be int64 addresses")
+    if generated is not None and (generated.dtype != torch.int32 or generated.shape != (inputs.n_requests,)):
+        raise ValueError("generated must be int32 [B]")
+    if generated is not None and outputs.kv_indices is None:
+        raise ValueError("generated entries need kv_indices outputs")
+    lib = _lib.load()
+    device = req_to_token.device
+    with _on_device(device):
+        rc = lib.akv_compact_rows(
+            inputs.n_requests,
+            inputs.req_offsets.data_ptr(),
+            inputs.max_tokens,
+            req_to_token.data_ptr(),
+            req_to_token.stride(0),
+            _lib.ptr(row_pointers),
+            req_rows.data_ptr(),
+            inputs.keep.data_ptr(),
+            inputs.birth_positions.data_ptr(),
+            inputs.final_positions.data_ptr(),
+            _lib.ptr(fresh_slots) if inputs.moved_total else None,
+            inputs.moved_total,
+            outputs.retired.data_ptr(),
+            outputs.retired.numel(),
+            outputs.copy_src.data_ptr(),
+            outputs.copy_dst.data_ptr(),
+            outputs.copy_pairs.data_ptr(),
+            outputs.raw_indices.data_ptr(),
+            outputs.active_positions.data_ptr(),
+            outputs.raw_indices.numel(),
+            _lib.ptr(generated),
+            _lib.ptr(outputs.kv_indices),
+            outputs.kv_indices.numel() if outputs.kv_indices is not None else 0,
+            _lib.ptr(outputs.kv_indptr),
+            outputs.counts.data_ptr(),
+            outputs.workspace.data_ptr(),
+            outputs.workspace.numel() * 8,
+            outputs.status.data_ptr(),
+            current_stream_handle(device),
+        )
+    _lib.check(rc, "akv_compact_rows")
+    return outputs

@@ -1,0 +1,295 @@
+"""Benchmark: Drop + Reposition of retained KV on one MI355X.
+
+Workload: one GPT-OSS-120B-shaped request (36 layers, 8 KV heads, head_dim
+64, bf16 K/V ~ N(0, 1), YaRN RoPE theta 150000 / factor 32 / original 4096,
+page size 1) of 32768 tokens dropping 12 seeded spans (~40%), then one
+Reposition.  Synthetic data; all inputs resident in HBM before timing.
+
+One step = the whole GPU side of the hot path:
+  birth-row write (D2D) -> page-table compaction (terminal row, freed
+  slots, copy lists, decode layout, kv_indptr / kv_indices) -> all-layer
+  Reposition (K re-rotation + V move, one launch) .
+``value`` = retained-KV bytes moved (K and V, read + write) per step / step
+time.  Also reported: p50 / p99 latency of the step and of the Reposition
+kernel alone with the 256 MB MALL flushed before each timed iteration, the
+Reposition kernel's roofline against 8 TB/s, and the CPU oracle on a bounded
+sample of the same workload.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from akv_amd import ops, synth, tables  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Reposition retained-KV GB/s (% HBM peak) + p50 latency, 32k GPT-OSS-shaped"
+PMC_SUMMARY = ROOT / "profiles" / "reposition_gpt-oss-32k_pmc.txt"
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--workload", default="gpt-oss-32k")
+    p.add_argument("--latency-iters", type=int, default=100)
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--reposition-only", action="store_true",
+                   help="time only the Reposition launch (for profiling runs)")
+    return p.parse_args()
+
+
+class Pipeline:
+    def __init__(self, name, device):
+        self.device = device
+        w = self.w = synth.workload(name)
+        if w.n_requests != 1:
+            raise SystemExit("the bench workload must be a single request")
+        m = w.model
+        t0 = time.perf_counter()
+        self.layouts = synth.compile_layouts(w)
+        self.compile_s = time.perf_counter() - t0
+        lay = self.layouts[0]
+        slots = synth.assign_slots(w, self.layouts)
+        self.slots = slots
+        n = w.lengths[0]
+        self.n = n
+        self.moved = slots.moved[0]
+        self.kept = int(lay.keep_mask.sum())
+        # request table: row 0 keeps the pristine birth row, row 1 is the live one
+        table = torch.full((2, n + 8), -1, dtype=torch.int32)
+        table[0, :n] = torch.from_numpy(slots.birth_rows[0])
+        table[0, n] = int(slots.birth_rows[0][-1])  # first generated token's slot
+        self.table = table.to(device)
+        self.rows = torch.tensor([1], dtype=torch.int64, device=device)
+        self.inputs = tables.pack_compaction_inputs(self.layouts, device)
+        self.out = tables.allocate_outputs(self.inputs, device, generated_total=1)
+        self.generated = torch.ones(1, dtype=torch.int32, device=device)
+        self.fresh = torch.from_numpy(slots.fresh[0]).to(device)
+        self.pool = synth.make_pool(m, w.pool_slots, device, seed=0, generate_on_device=True)
+        self.rope = synth.rope_table(w, device)
+        self.stream = torch.cuda.current_stream(device)
+        # scratch that evicts the 256 MB MALL between timed iterations
+        self.flush_buf = torch.empty(1 << 28, dtype=torch.float32, device=device)
+        kv_bytes = 2  # bf16
+        self.retained_bytes = self.moved * 4 * m.n_layers * m.n_heads * m.head_dim * kv_bytes
+        self.alg_bytes = self.retained_bytes + self.moved * 16 + self.moved * 2 * m.rotary_dim * 4
+
+    def compaction(self):
+        self.table[1].copy_(self.table[0])
+        tables.compact_rows(self.inputs, self.table, self.rows, self.fresh, self.out, generated=self.generated)
+
+    def reposition(self):
+        p, o = self.pool, self.out
+        ops.reposition_kv_layers(p.k_ptrs, p.v_ptrs, p.k[0], p.v[0], o.copy_src, o.copy_dst, o.copy_pairs,
+                                 self.rope, is_neox_style=self.w.model.is_neox_style)
+
+    def step(self):
+        self.compaction()
+        self.reposition()
+
+    def flush(self):
+        self.flush_buf.fill_(1.0)
+
+
+def read_pmc_traffic():
+    """HBM bytes per Reposition launch from the committed rocprof PMC summary."""
+    if not PMC_SUMMARY.exists():
+        return None
+    for line in PMC_SUMMARY.read_text().splitlines():
+        if line.startswith("hbm_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(pipe, seconds):
+    """The CPU oracle (numpy port of the reference path) on a bounded sample."""
+    from oracle import events as oe
+    from oracle import occurrence as occ
+    from oracle import reposition as rp
+
+    w, lay = pipe.w, pipe.layouts[0]
+    m = w.model
+    ev = synth.request_events(pipe.n, w.spans[0])
+    t0 = time.perf_counter()
+    ref = oe.compile_context_layout(*(ev[k].numpy() for k in ev))
+    compile_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    cf = occ.closed_form(pipe.slots.birth_rows[0], ref.keep_mask, ref.birth_positions, ref.positions,
+                         pipe.slots.fresh[0])
+    tables_s = time.perf_counter() - t0
+    # Reposition on a sample of moved tokens across all layers: gather the
+    # sample's source rows into a compact host pool and move them with the oracle
+    rng = np.random.default_rng(0)
+    table = pipe.rope.cpu().numpy()
+    src_all = cf["copy_source_slots"]
+    pairs_all = cf["copy_position_pairs"]
+
+    def run(count):
+        idx = np.sort(rng.choice(len(src_all), size=count, replace=False))
+        s = torch.from_numpy(src_all[idx].astype(np.int64)).to(pipe.device)
+        k = [t[s].cpu().view(torch.int16).numpy().view(np.uint16) for t in pipe.pool.k]
+        v = [t[s].cpu().view(torch.int16).numpy().view(np.uint16) for t in pipe.pool.v]
+        k = [np.concatenate((x, np.zeros_like(x))) for x in k]
+        v = [np.concatenate((x, np.zeros_like(x))) for x in v]
+        t = time.perf_counter()
+        rp.reposition_kv_layers(k, v, np.arange(count), np.arange(count, 2 * count), pairs_all[idx], table,
+                                dtype="bf16")
+        return time.perf_counter() - t
+
+    probe = min(256, len(src_all))
+    dt = run(probe)
+    per_token = dt / probe
+    count = int(min(len(src_all), max(probe, seconds / max(per_token, 1e-9))))
+    dt = run(count)
+    per_token = dt / count
+    full_s = compile_s + tables_s + per_token * len(src_all)
+    bytes_per_token = 4 * m.n_layers * m.n_heads * m.head_dim * 2
+    return {
+        "value": round(bytes_per_token * count / dt / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"numpy oracle, single thread: Reposition of {count} of {len(src_all)} moved tokens x "
+                   f"{m.n_layers} layers ({dt:.2f} s); event compile {compile_s * 1e3:.1f} ms and table "
+                   f"closed form {tables_s * 1e3:.1f} ms on the full request; full-request estimate "
+                   f"{full_s * 1e3:.0f} ms"),
+        "full_request_ms_estimate": round(full_s * 1e3, 1),
+        "host": host_info(),
+    }
+
+
+def host_info():
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu": model, "logical_cpus": os.cpu_count(), "torch_threads": torch.get_num_threads()}
+
+
+def percentile(xs, q):
+    return float(np.percentile(np.asarray(xs), q))
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported here "
+              "(the Drop + Reposition path shards by KV head under TP with no communication)", file=sys.stderr)
+        raise SystemExit(2)
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    pipe = Pipeline(args.workload, device)
+    run = pipe.reposition if args.reposition_only else pipe.step
+    pipe.compaction()
+    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    print(f"# warmup done: {args.warmup} steps", file=sys.stderr, flush=True)
+
+    # throughput: K back-to-back steps
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        run()
+    end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ms_per_step = start.elapsed_time(end) / args.steps
+    print(f"# timed {args.steps} steps: {ms_per_step:.4f} ms/step (wall {wall_ms:.1f} ms)", file=sys.stderr, flush=True)
+
+    # latency with a cold MALL: events around the whole step and the Reposition alone
+    step_ms, repo_ms = [], []
+    for _ in range(args.latency_iters):
+        pipe.flush()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e2 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        if not args.reposition_only:
+            pipe.compaction()
+        e1.record()
+        pipe.reposition()
+        e2.record()
+        torch.cuda.synchronize()
+        step_ms.append(e0.elapsed_time(e2))
+        repo_ms.append(e1.elapsed_time(e2))
+    print(f"# latency iterations done: {args.latency_iters}", file=sys.stderr, flush=True)
+
+    repo_avg_s = float(np.mean(repo_ms)) / 1e3
+    achieved = pipe.alg_bytes / repo_avg_s / 1e9
+    traffic = read_pmc_traffic()
+    m = pipe.w.model
+    result = {
+        "metric": METRIC,
+        "value": round(pipe.retained_bytes / (ms_per_step / 1e3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": pipe.w.name,
+            "layers": m.n_layers,
+            "kv_heads": m.n_heads,
+            "head_dim": m.head_dim,
+            "kv_dtype": "bf16",
+            "rope": "yarn(theta=150000, factor=32, original=4096)",
+            "tokens": pipe.n,
+            "kept": pipe.kept,
+            "moved": pipe.moved,
+            "page_size": 1,
+            "step": "reposition only" if args.reposition_only else "birth-row write + compaction + reposition",
+        },
+        "p50_ms": round(percentile(step_ms, 50), 5),
+        "p99_ms": round(percentile(step_ms, 99), 5),
+        "reposition_p50_ms": round(percentile(repo_ms, 50), 5),
+        "reposition_p99_ms": round(percentile(repo_ms, 99), 5),
+        "pct_hbm_peak": round(100 * pipe.retained_bytes / (percentile(repo_ms, 50) / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
+        "launches_per_step": 1 if args.reposition_only else 5,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "reposition_vec_kernel<bf16, f32, neox>",
+            "bytes_per_launch": pipe.alg_bytes,
+        },
+    }
+    if not args.no_cpu_baseline:
+        print("# cpu baseline ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(pipe, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

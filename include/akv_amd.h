@@ -1,0 +1,217 @@
+/*
+ * akv_amd -- C ABI of the MI355X (gfx950) Drop + Reposition hot path.
+ *
+ * Plain C: raw pointers, sizes and a HIP stream handle (void*, NULL = the
+ * default stream).  No entry point allocates device memory, frees it,
+ * synchronises the stream or reads device memory back to the host: every
+ * compute entry point only validates its host-visible arguments and enqueues
+ * kernels on `stream`.  Device buffers must stay alive until the stream has
+ * finished with them (the caller's lifetime contract).
+ *
+ * Return value: 0 on success, AKV_EINVAL for an invalid argument, AKV_EHIP
+ * when the HIP runtime rejected a launch.  akv_last_error() returns the
+ * message of the last failure on the calling thread.
+ *
+ * Paths in the citations are relative to the reference repository root.
+ */
+#ifndef AKV_AMD_H
+#define AKV_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AKV_OK 0
+#define AKV_EINVAL (-22)
+#define AKV_EHIP (-5)
+
+/* Storage dtypes of KV buffers and RoPE tables. */
+#define AKV_F32 0
+#define AKV_F16 1
+#define AKV_BF16 2
+
+/* Integer dtypes of index vectors. */
+#define AKV_I32 0
+#define AKV_I64 1
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* akv_last_error(void);
+
+/* Library version string. */
+const char* akv_version(void);
+
+/*
+ * Fused all-layer Reposition: for every token t and layer l of the group,
+ * re-rotate the rotary part of K from position pairs[t][0] to pairs[t][1]
+ * (fp32, inverse rotation then forward rotation, IEEE division, no FMA
+ * contraction, round-to-nearest-even store), copy the non-rotary K tail and
+ * all of V, from slot src[t] to slot dst[t].  k_ptrs/v_ptrs are DEVICE
+ * arrays of n_layers base addresses of [slots, heads, head_dim] buffers
+ * that share the given element strides.
+ *
+ * Replaces reposition_kv_layers / _reposition_layers_kernel,
+ * akv/system/sglang/kernels/ops/attention/context_reposition.py:126-236
+ * (kernel :28-123).
+ */
+int akv_reposition_kv_layers(const uint64_t* k_ptrs, const uint64_t* v_ptrs,
+                             int32_t n_layers, int32_t kv_dtype,
+                             int32_t n_heads, int32_t head_dim,
+                             int32_t rotary_dim, int64_t k_stride_slot,
+                             int64_t k_stride_head, int64_t v_stride_slot,
+                             int64_t v_stride_head, const int32_t* src,
+                             const int32_t* dst, const int32_t* pairs,
+                             int64_t pair_stride, int64_t n_tokens,
+                             const void* cos_sin, int32_t cos_sin_dtype,
+                             int64_t rope_stride, int32_t is_neox,
+                             int32_t skip_unmapped, void* stream);
+
+/*
+ * Device bytes of the scratch buffer akv_compact_rows needs for a batch of
+ * n_requests whose longest request has max_tokens raw tokens.
+ */
+int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t max_tokens);
+
+/*
+ * Batched page-table compaction of a single-owner final forward.  For
+ * request b, raw tokens [req_offsets[b], req_offsets[b+1]) of the flat
+ * keep / birth_positions / final_positions vectors; its raw row is
+ * row_pointers[req_rows[b]] when row_pointers != NULL, else
+ * table + req_rows[b] * row_stride, and holds the birth slots on entry.
+ * A kept token is "moved" when its final position differs from its birth
+ * position; moved tokens take fresh_slots in request-major raw order.
+ * Outputs (flat, request-major, raw order):
+ *   raw row (in place)  keep ? (moved ? fresh : birth) : -1
+ *   retired             birth slots of dropped or moved tokens
+ *   copy_src/copy_dst/copy_pairs   the Reposition inputs (pairs [M,2])
+ *   raw_indices/active_positions   decode layout of kept tokens
+ *   kv_indices (opt.)   compacted rows, then generated[b] raw-row entries
+ *                       after the prompt, laid out by kv_indptr
+ *   kv_indptr  (opt.)   [B+1] exclusive scan of kept + generated
+ *   counts     (opt.)   [B,3] kept, moved, retired
+ *   status     (opt.)   device int32, set to 1 if fresh_count or a
+ *                       capacity does not match (outputs are then partial)
+ * Replaces the CPU numpy/H2D path of OccurrenceState.advance +
+ * terminal_slots + ReqToTokenPool.write + ContextDecodeLayout.from_layout,
+ * akv/system/sglang/srt/context_system/occurrence.py:47-66,632-767 and
+ * akv/system/sglang.patch:3161-3164,4230-4235; request_active_slots,
+ * akv/system/sglang/srt/disaggregation/context_transfer.py:110-128.
+ */
+int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets,
+                     int64_t max_tokens, int32_t* table, int64_t row_stride,
+                     const int64_t* row_pointers, const int64_t* req_rows,
+                     const uint8_t* keep, const int32_t* birth_positions,
+                     const int32_t* final_positions, const int32_t* fresh_slots,
+                     int64_t fresh_count, int32_t* retired,
+                     int64_t retired_capacity, int32_t* copy_src,
+                     int32_t* copy_dst, int32_t* copy_pairs,
+                     int32_t* raw_indices, int32_t* active_positions,
+                     int64_t kept_capacity, const int32_t* generated,
+                     int32_t* kv_indices, int64_t kv_capacity,
+                     int32_t* kv_indptr, int32_t* counts, void* workspace,
+                     int64_t workspace_bytes, int32_t* status, void* stream);
+
+/*
+ * Decode read indices over raw request rows through the registry rows
+ * int64 [rows, 6] = (raw_ids_ptr, positions_ptr, prompt_len, active,
+ * next_pos, row_ptr):
+ *   out[indptr[b] + i] = T(row[raw]), raw = raw_ids[start+i] if start+i <
+ *   active else prompt + start + i - active (raw = start + i when raw_ids_ptr
+ *   is 0); T(x) = mapping[x] * multiplier when mapping != NULL.
+ * rows/lengths/indptr/output/starts/mapping take AKV_I32 or AKV_I64.
+ * Replaces context_decode_indices,
+ * akv/system/sglang/kernels/ops/attention/context_page_table.py:34-76.
+ */
+int akv_decode_indices(const int64_t* registry, const int32_t* table,
+                       int64_t row_stride, const void* rows, int32_t rows_dtype,
+                       const void* lengths, int32_t lengths_dtype,
+                       const void* indptr, int32_t indptr_dtype, void* output,
+                       int32_t output_dtype, const void* starts,
+                       int32_t starts_dtype, const void* mapping,
+                       int32_t mapping_dtype, int64_t multiplier,
+                       int32_t n_requests, void* stream);
+
+/*
+ * Sliding-window visible key counts (inclusive q_pos - k_pos <= window),
+ * by binary search over the compacted positions of each registry row;
+ * min(length, window) for ordinary rows.  When starts != NULL it also
+ * writes starts[b] = lengths[b] - output[b] (same dtype as lengths).
+ * Replaces context_window_lengths,
+ * akv/system/sglang/kernels/ops/attention/context_page_table.py:7-31
+ * (and the starts of context_backend.py:792,807).
+ */
+int akv_window_lengths(const int64_t* registry, const void* rows,
+                       int32_t rows_dtype, const void* lengths,
+                       int32_t lengths_dtype, void* output,
+                       int32_t output_dtype, void* starts, int64_t window,
+                       int32_t n_requests, void* stream);
+
+/*
+ * indptr[0] = 0, indptr[b+1] = sum(lengths[0..b]); when last_page_len !=
+ * NULL also last_page_len[b] = ((lengths[b] - 1) % page_size) + 1 (0 for
+ * an empty request).  indptr_scale != 1 instead writes the page-table form
+ * indptr[b] = b * indptr_scale (lengths unused).
+ * Replaces kv_indptr[1:] = cumsum(seq_lens), akv/system/sglang.patch:2266-2268,
+ * and the fill_table indptr, context_backend.py:793.
+ */
+int akv_build_indptr(const void* lengths, int32_t lengths_dtype,
+                     int32_t n_requests, void* indptr, int32_t indptr_dtype,
+                     int32_t* last_page_len, int32_t page_size,
+                     int64_t indptr_scale, void* stream);
+
+/*
+ * Side-row scatter: ((int32_t*)pointers[rows[i]])[columns[i]] = values[i].
+ * Replaces write_row_slots, akv/system/sglang/kernels/ops/memory/context_rows.py:7-15.
+ */
+int akv_write_row_slots(const int64_t* pointers, const void* rows,
+                        int32_t rows_dtype, const void* columns,
+                        int32_t columns_dtype, const void* values,
+                        int32_t values_dtype, int64_t n, void* stream);
+
+/*
+ * Host event compiler (CPU, no device work).  Replays Drop and Reposition
+ * events over the raw token stream.  Two calls, like the reference's count
+ * and fill passes: akv_plan_count returns the number of transitions through
+ * *transition_count (status 0), or status 1 with *bad_boundary set when a
+ * Reposition has no active token.  akv_plan_compile fills caller-provided
+ * host arrays; status 2 with *bad_token when a token id is outside
+ * [0, INT32_MAX].  Invalid event metadata returns AKV_EINVAL with the
+ * reference's message in akv_last_error().
+ * Replaces count_radix_reposition_transitions and
+ * compile_radix_reposition_layout,
+ * akv/system/sglang/kernels/ops/attention/context_plan.py:80-532.
+ */
+int akv_plan_count(int64_t token_count, const int32_t* drop_insert_offsets,
+                   int64_t drop_count, const int32_t* drop_range_offsets,
+                   const int32_t* drop_ranges, int64_t drop_ranges_len,
+                   const int32_t* reposition_raw_boundaries,
+                   const int32_t* reposition_insert_offsets,
+                   int64_t reposition_count, int32_t* transition_counts,
+                   int64_t* status);
+
+int akv_plan_compile(const void* token_ids, int32_t token_ids_dtype,
+                     int64_t token_count, const int32_t* drop_insert_offsets,
+                     int64_t drop_count, const int32_t* drop_range_offsets,
+                     const int32_t* drop_ranges, int64_t drop_ranges_len,
+                     const int32_t* reposition_raw_boundaries,
+                     const int32_t* reposition_insert_offsets,
+                     int64_t reposition_count, int32_t* records,
+                     uint8_t* virtual_mask, int64_t* key_to_token,
+                     int64_t record_capacity, int64_t* token_to_key,
+                     int32_t* positions, uint8_t* keep_mask,
+                     int32_t* materialized_stage, int32_t* birth_positions,
+                     int32_t* birth_stages, int32_t* transition_offsets,
+                     int32_t* transition_raw_tokens,
+                     int32_t* transition_old_positions,
+                     int32_t* transition_new_positions,
+                     int64_t transition_capacity,
+                     int32_t* effective_reposition_stages,
+                     int64_t* drop_event_to_key, uint8_t* effective_repositions,
+                     uint8_t* ignored_repositions, int64_t* status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AKV_AMD_H */

@@ -1,0 +1,33 @@
+"""CPU oracle for the Drop + Reposition hot path -- TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU, what the reference computes on the path
+that the HIP library replaces.  It is the checker: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it.  The product (``akv_amd``) never imports, links or calls anything
+here, and it has no CPU fallback: when the HIP library is missing it raises.
+
+Modules and the reference code each one restates (paths relative to the
+reference repository root):
+
+``bf16``        IEEE round-to-nearest-even fp32 -> bf16/fp16 packing used by
+                every store of the Reposition kernel (Triton's default
+                downcast, ``context_reposition.py:103-112``).
+``reposition``  ``_reposition_layers_kernel`` op order
+                (``akv/system/sglang/kernels/ops/attention/context_reposition.py:54-123``)
+                and the wrapper's validation (``:126-236``).
+``events``      the linked-list Drop/Reposition replay of
+                ``akv/system/sglang/kernels/ops/attention/context_plan.py:80-532``
+                and its driver ``akv/system/sglang/srt/context_system/ir.py:113-274``.
+``occurrence``  the final-forward ownership result of
+                ``akv/system/sglang/srt/context_system/occurrence.py:112-265,341-466,632-767``
+                (terminal row, retired slots, copy lists, decode layout).
+``decode``      ``context_decode_indices`` / ``context_window_lengths``
+                (``akv/system/sglang/kernels/ops/attention/context_page_table.py:7-76``),
+                ``write_row_slots`` (``.../ops/memory/context_rows.py:7-15``) and the
+                ``kv_indptr = cumsum`` rebuild (``akv/system/sglang.patch:2266-2268``).
+
+How each function is pinned (golden vectors / closed forms / brute force /
+invariants) is stated in its module docstring.  The RoPE tables are not part
+of the oracle: the kernel and the oracle read the same table, so parity of
+the kernel holds for any table.
+"""

@@ -1,0 +1,145 @@
+"""CPU checks of libakv_amd.so: exports, argument validation, host compiler.
+
+No kernel is launched here; the event compiler is host code.
+"""
+
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from akv_amd import _lib, plan, synth
+from oracle import events as oe
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "akv_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(akv_\w+)\(", text, flags=re.M)))
+
+
+def test_exports_every_declared_symbol(lib):
+    declared = _declared()
+    assert len(declared) >= 10
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_lib.EXPORTED)
+    assert lib.akv_version().decode().startswith("akv_amd")
+
+
+def test_validation_rejects_before_any_device_work(lib):
+    rc = lib.akv_reposition_kv_layers(None, None, 1, 7, 8, 64, 64, 512, 64, 512, 64, None, None, None, 2,
+                                      1, None, 0, 64, 1, 0, None)
+    assert rc == _lib.AKV_EINVAL and "KV dtype" in _lib.last_error()
+    rc = lib.akv_reposition_kv_layers(None, None, 1, 2, 8, 64, 63, 512, 64, 512, 64, None, None, None, 2,
+                                      1, None, 0, 64, 1, 0, None)
+    assert rc == _lib.AKV_EINVAL and "rotary_dim" in _lib.last_error()
+    # empty work returns silently, like the reference
+    assert lib.akv_reposition_kv_layers(None, None, 0, 2, 8, 64, 64, 512, 64, 512, 64, None, None, None, 2,
+                                        0, None, 0, 64, 1, 0, None) == 0
+    def zeros(fn, **overrides):
+        args = [None if t is _lib.c_void_p else 0 for t in fn.argtypes]
+        for i, v in overrides.items():
+            args[int(i[1:])] = v
+        return args
+
+    assert lib.akv_compact_rows(*zeros(lib.akv_compact_rows, a0=-1)) == _lib.AKV_EINVAL
+    assert lib.akv_compact_rows(*zeros(lib.akv_compact_rows, a0=2)) == _lib.AKV_EINVAL
+    assert "null device pointer" in _lib.last_error()
+    ws = lib.akv_compact_workspace_bytes(64, 65536)
+    assert ws > 0
+    assert lib.akv_decode_indices(*zeros(lib.akv_decode_indices)) == 0
+    assert lib.akv_decode_indices(*zeros(lib.akv_decode_indices, a16=3)) == _lib.AKV_EINVAL
+    assert lib.akv_build_indptr(None, 0, 3, None, 0, None, 1, 1, None) == _lib.AKV_EINVAL
+
+
+def _events(n, drops, repos):
+    insert = [i for i, _ in drops]
+    offsets, flat = [0], []
+    for _, ranges in drops:
+        for s, e in ranges:
+            flat += [s, e]
+        offsets.append(offsets[-1] + len(ranges))
+    b = torch.tensor(repos, dtype=torch.int32)
+    return dict(
+        token_ids=torch.arange(n, dtype=torch.int64) * 7 % 1000,
+        drop_insert_offsets=torch.tensor(insert, dtype=torch.int32),
+        drop_range_offsets=torch.tensor(offsets, dtype=torch.int32),
+        drop_ranges=torch.tensor(flat, dtype=torch.int32),
+        reposition_raw_boundaries=b,
+        reposition_insert_offsets=b + 1,
+    )
+
+
+FIELDS = ["positions", "keep_mask", "birth_positions", "birth_stages", "materialized_stage",
+          "transition_offsets", "transition_raw_tokens", "transition_old_positions",
+          "transition_new_positions", "effective_reposition_stages", "effective_repositions",
+          "ignored_repositions", "drop_event_to_key", "records", "virtual_mask", "key_to_token",
+          "token_to_key"]
+
+
+def _compare(ev):
+    got = plan.compile_context_layout(**ev)
+    want = oe.compile_context_layout(*(ev[k].numpy() for k in ev))
+    for f in FIELDS:
+        np.testing.assert_array_equal(getattr(got, f).numpy(), getattr(want, f), err_msg=f)
+    assert got.next_position == want.next_position
+
+
+def test_native_compiler_matches_oracle_on_random_programs():
+    rng = np.random.default_rng(7)
+    done = 0
+    for _ in range(300):
+        n = int(rng.integers(1, 90))
+        drops = []
+        for at in sorted(rng.choice(np.arange(1, n + 1), size=min(n, int(rng.integers(0, 5))), replace=False)):
+            cuts = np.sort(rng.choice(np.arange(0, at + 1), size=min(4, at + 1), replace=False))
+            ranges = [(int(cuts[i]), int(cuts[i + 1])) for i in range(0, len(cuts) - 1, 2)]
+            drops.append((int(at), ranges))
+        repos = sorted(rng.choice(np.arange(0, n), size=min(n, int(rng.integers(0, 5))), replace=False).tolist())
+        ev = _events(n, drops, repos)
+        try:
+            oe.compile_context_layout(*(ev[k].numpy() for k in ev))
+        except ValueError as err:
+            with pytest.raises(ValueError, match=re.escape(str(err))):
+                plan.compile_context_layout(**ev)
+            continue
+        _compare(ev)
+        done += 1
+    assert done > 150
+
+
+def test_native_compiler_matches_oracle_on_workloads():
+    for name in ("tiny", "gpt-oss-32k"):
+        w = synth.workload(name)
+        _compare(synth.request_events(w.lengths[0], w.spans[0]))
+
+
+@pytest.mark.parametrize(
+    "kw,message",
+    [
+        (dict(drop_ranges=torch.tensor([0, 1], dtype=torch.int32)), "drop_range_offsets does not cover drop_ranges"),
+        (dict(reposition_insert_offsets=torch.tensor([3], dtype=torch.int32)), "Invalid Reposition event metadata"),
+        (dict(token_ids=torch.zeros((2, 2), dtype=torch.int32)), "token_ids must be a one-dimensional CPU integer tensor."),
+        (dict(drop_ranges=torch.tensor([2**40, 0], dtype=torch.int64),
+              drop_range_offsets=torch.tensor([0, 1], dtype=torch.int32),
+              drop_insert_offsets=torch.tensor([5], dtype=torch.int32)), "drop_ranges exceeds the signed int32 range."),
+    ],
+)
+def test_native_compiler_error_messages(kw, message):
+    ev = _events(8, [], [5])
+    ev.update(kw)
+    with pytest.raises(ValueError, match=re.escape(message)):
+        plan.compile_context_layout(**ev)
+
+
+def test_append_generated_layout():
+    ev = _events(10, [(10, [(2, 4)])], [9])
+    lay = plan.compile_context_layout(**ev)
+    ext = plan.append_generated_layout(lay, [5, 6, 7])
+    assert ext.next_position == lay.next_position + 3
+    assert ext.positions[-3:].tolist() == [8, 9, 10]
+    assert ext.keep_mask[-3:].all()

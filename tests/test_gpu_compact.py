@@ -1,0 +1,134 @@
+"""GPU parity of the batched page-table compaction against the oracle.
+
+Integer outputs must be bit-exact: terminal rows (in place), retired slots,
+copy lists, decode layouts, compacted rows / kv_indices and kv_indptr.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from akv_amd import synth, tables
+from oracle import occurrence as occ
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(device, w, layouts, *, generated=None, side_rows=False, width_extra=8):
+    slots = synth.assign_slots(w, layouts)
+    inputs = tables.pack_compaction_inputs(layouts, device)
+    width = max(w.lengths) + width_extra
+    pool_rows = w.n_requests + 3
+    table = torch.full((pool_rows, width), -5, dtype=torch.int32)
+    rng = np.random.default_rng(w.seed)
+    req_rows = rng.permutation(np.arange(pool_rows))[: w.n_requests]
+    gen = generated if generated is not None else [0] * w.n_requests
+    tails = []
+    for b, row in enumerate(req_rows):
+        n = w.lengths[b]
+        table[row, :n] = torch.from_numpy(slots.birth_rows[b])
+        tail = rng.integers(1, 10**6, size=gen[b]).astype(np.int32)
+        table[row, n : n + gen[b]] = torch.from_numpy(tail)
+        tails.append(tail)
+    table = table.to(device)
+    row_pointers = None
+    side = {}
+    if side_rows:
+        # every request lives in its own side row, outside the table
+        ptrs = torch.tensor([table[r].data_ptr() for r in range(pool_rows)], dtype=torch.int64)
+        for b, row in enumerate(req_rows):
+            side[row] = table[row].clone()
+            ptrs[row] = side[row].data_ptr()
+        row_pointers = ptrs.to(device)
+    fresh = torch.from_numpy(np.concatenate(slots.fresh).astype(np.int32) if slots.fresh else np.zeros(0, np.int32)).to(device)
+    return slots, inputs, table, torch.from_numpy(req_rows.astype(np.int64)).to(device), fresh, row_pointers, side, tails
+
+
+def _check(w, layouts, slots, out, rows_after, tails, gen):
+    kept_off = moved_off = retired_off = kv_off = 0
+    indptr = out.kv_indptr.cpu().numpy() if out.kv_indptr is not None else None
+    counts = out.counts.cpu().numpy()
+    for b, lay in enumerate(layouts):
+        want = occ.closed_form(slots.birth_rows[b], lay.keep_mask.numpy(), lay.birth_positions.numpy(),
+                               lay.positions.numpy(), slots.fresh[b])
+        n = w.lengths[b]
+        kept = len(want["raw_indices"])
+        moved = len(want["copy_source_slots"])
+        retired = len(want["retired_slots"])
+        np.testing.assert_array_equal(rows_after[b][:n], want["terminal_row"], err_msg=f"row {b}")
+        np.testing.assert_array_equal(out.retired.cpu().numpy()[retired_off : retired_off + retired], want["retired_slots"])
+        np.testing.assert_array_equal(out.copy_src.cpu().numpy()[moved_off : moved_off + moved], want["copy_source_slots"])
+        np.testing.assert_array_equal(out.copy_dst.cpu().numpy()[moved_off : moved_off + moved], want["copy_destination_slots"])
+        np.testing.assert_array_equal(out.copy_pairs.cpu().numpy()[moved_off : moved_off + moved], want["copy_position_pairs"])
+        np.testing.assert_array_equal(out.raw_indices.cpu().numpy()[kept_off : kept_off + kept], want["raw_indices"])
+        np.testing.assert_array_equal(out.active_positions.cpu().numpy()[kept_off : kept_off + kept], want["active_positions"])
+        assert counts[b].tolist() == [kept, moved, retired]
+        if out.kv_indices is not None:
+            assert indptr[b] == kv_off
+            seg = out.kv_indices.cpu().numpy()[kv_off : kv_off + kept + gen[b]]
+            np.testing.assert_array_equal(seg, np.concatenate((want["active_slots"], tails[b])))
+            kv_off += kept + gen[b]
+        kept_off += kept
+        moved_off += moved
+        retired_off += retired
+    if indptr is not None:
+        assert indptr[-1] == kv_off
+    assert out.status.item() == 0
+
+
+def _run(device, w, *, generated=None, side_rows=False):
+    layouts = synth.compile_layouts(w)
+    slots, inputs, table, req_rows, fresh, row_pointers, side, tails = _setup(
+        device, w, layouts, generated=generated, side_rows=side_rows)
+    gen = generated if generated is not None else [0] * w.n_requests
+    out = tables.allocate_outputs(inputs, device, generated_total=sum(gen))
+    gen_t = torch.tensor(gen, dtype=torch.int32, device=device) if generated is not None else None
+    table_before = table.clone()
+    tables.compact_rows(inputs, table, req_rows, fresh, out, row_pointers=row_pointers, generated=gen_t)
+    torch.cuda.synchronize()
+    rows = req_rows.cpu().numpy()
+    if side_rows:
+        rows_after = [side[r].cpu().numpy() for r in rows]
+        # with side rows the table itself is untouched
+        assert torch.equal(table, table_before)
+    else:
+        rows_after = [table[r].cpu().numpy() for r in rows]
+    _check(w, layouts, slots, out, rows_after, tails, gen)
+    return out
+
+
+def test_tiny_single_request(device):
+    _run(device, synth.workload("tiny"))
+
+
+def test_gpt_oss_32k(device):
+    _run(device, synth.workload("gpt-oss-32k"), generated=[1])
+
+
+def test_ragged_batch_64(device):
+    w = synth.workload("ragged-64")
+    _run(device, w, generated=[int(x) for x in np.random.default_rng(5).integers(1, 9, size=w.n_requests)])
+
+
+def test_side_rows_and_edge_requests(device):
+    model = synth.TINY
+    # no drop; drop only at the tail (ignored Reposition); drop at the head;
+    # almost everything dropped; a 1-token request; a tile-boundary length
+    lengths = (50, 64, 70, 5000, 1, 4096 + 17)
+    spans = ((), ((60, 64),), ((0, 10),), ((1, 4999),), (), ((4095, 4097), (4100, 4101)))
+    w = synth.Workload("edges", model, lengths, spans, seed=11, table_positions=5000, pool_slots=40000)
+    _run(device, w, side_rows=True, generated=[2, 0, 1, 3, 1, 0])
+
+
+def test_fresh_count_mismatch_sets_status(device):
+    w = synth.workload("tiny")
+    layouts = synth.compile_layouts(w)
+    slots, inputs, table, req_rows, fresh, row_pointers, side, tails = _setup(device, w, layouts)
+    out = tables.allocate_outputs(inputs, device)
+    # claim one fresh slot fewer than there are moved tokens
+    inputs.moved = (inputs.moved[0] - 1,)
+    out.copy_src, out.copy_dst = out.copy_src[:-1], out.copy_dst[:-1]
+    out.copy_pairs = out.copy_pairs[:-1]
+    tables.compact_rows(inputs, table, req_rows, fresh[:-1], out)
+    torch.cuda.synchronize()
+    assert out.status.item() == 1

@@ -1,0 +1,203 @@
+"""GPU parity of the fused Reposition kernel against the CPU oracle.
+
+Bit-exact for K, V and every untouched slot, across dtypes, pair styles,
+partial rotary widths, strides, pointer alignment and the full 32k GPT-OSS
+shape (sampled oracle check + size-independent properties at full size).
+"""
+
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from akv_amd import ops, synth
+from akv_amd.rope import make_table
+from oracle import reposition as rp
+
+from helpers import ORACLE_DTYPE, single_request, storage_equal, to_storage
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_case(device, *, layers=2, heads=2, head_dim=64, rotary_dim=None, kv_dtype=torch.bfloat16,
+              table_dtype=torch.float32, neox=True, slots=512, moved=200, seed=0, skip_unmapped=False,
+              same_every=0, misalign=False, slot_stride_extra=0, table_kind="yarn"):
+    rotary_dim = rotary_dim or head_dim
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    width = head_dim * heads + slot_stride_extra
+    k_store, v_store, k_views, v_views = [], [], [], []
+    for _ in range(layers):
+        # a wider backing buffer gives non-contiguous slot strides when
+        # slot_stride_extra > 0, and a shifted base when misalign is set
+        kb = torch.randn((slots * width + 16,), generator=g).to(kv_dtype)
+        vb = torch.randn((slots * width + 16,), generator=g).to(kv_dtype)
+        kb, vb = kb.to(device), vb.to(device)
+        off = 1 if misalign else 0
+        k_views.append(kb[off : off + slots * width].view(slots, width)[:, : heads * head_dim].view(slots, heads, head_dim)
+                       if slot_stride_extra == 0 else
+                       torch.as_strided(kb, (slots, heads, head_dim), (width, head_dim, 1), off))
+        v_views.append(vb[off : off + slots * width].view(slots, width)[:, : heads * head_dim].view(slots, heads, head_dim)
+                       if slot_stride_extra == 0 else
+                       torch.as_strided(vb, (slots, heads, head_dim), (width, head_dim, 1), off))
+        k_store.append(kb)
+        v_store.append(vb)
+    perm = rng.permutation(np.arange(1, slots))
+    src = perm[:moved].astype(np.int32)
+    dst = perm[moved : 2 * moved].astype(np.int32)
+    if skip_unmapped:
+        src[::7] = 0
+        dst[3::11] = -1
+    positions = 300
+    old = rng.integers(0, positions, size=moved)
+    new = rng.integers(0, positions, size=moved)
+    if same_every:
+        new[::same_every] = old[::same_every]
+    pairs = np.stack((old, new), 1).astype(np.int32)
+    table = make_table(table_kind, rotary_dim, positions, base=150000.0, factor=32.0, original_max=4096) \
+        if table_kind == "yarn" else make_table("plain", rotary_dim, positions, base=10000.0)
+    table = table.to(table_dtype)
+
+    k_np = [to_storage(t) for t in k_views]
+    v_np = [to_storage(t) for t in v_views]
+    rp.reposition_kv_layers(k_np, v_np, src, dst, pairs, to_storage(table), dtype=ORACLE_DTYPE[kv_dtype],
+                            cos_sin_dtype=ORACLE_DTYPE[table_dtype], is_neox_style=neox,
+                            skip_unmapped=skip_unmapped, rotary_dim=rotary_dim)
+    k_ptrs = torch.tensor([t.data_ptr() for t in k_views], dtype=torch.uint64).to(device)
+    v_ptrs = torch.tensor([t.data_ptr() for t in v_views], dtype=torch.uint64).to(device)
+    ops.reposition_kv_layers(
+        k_ptrs, v_ptrs, k_views[0], v_views[0],
+        torch.from_numpy(src).to(device), torch.from_numpy(dst).to(device),
+        torch.from_numpy(pairs).to(device), table.to(device),
+        is_neox_style=neox, skip_unmapped=skip_unmapped, rotary_dim=rotary_dim,
+    )
+    torch.cuda.synchronize()
+    for layer in range(layers):
+        got_k, got_v = to_storage(k_views[layer]), to_storage(v_views[layer])
+        if not storage_equal(got_k, k_np[layer]):
+            diff = np.argwhere(got_k != k_np[layer])
+            raise AssertionError(f"K layer {layer}: {len(diff)} elements differ, first {diff[:5].tolist()}")
+        assert storage_equal(got_v, v_np[layer]), f"V layer {layer}"
+
+
+@pytest.mark.parametrize("neox", [True, False])
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_dtypes_and_styles(device, neox, kv_dtype):
+    _run_case(device, kv_dtype=kv_dtype, neox=neox, seed=1)
+
+
+@pytest.mark.parametrize("table_dtype", [torch.bfloat16, torch.float16])
+def test_half_precision_tables(device, table_dtype):
+    _run_case(device, table_dtype=table_dtype, seed=2)
+
+
+@pytest.mark.parametrize("rotary_dim", [32, 16, 48])
+def test_partial_rotary(device, rotary_dim):
+    _run_case(device, rotary_dim=rotary_dim, seed=3)
+    _run_case(device, rotary_dim=rotary_dim, neox=False, seed=4)
+
+
+@pytest.mark.parametrize("heads,head_dim,layers", [(8, 64, 36), (8, 128, 3), (4, 64, 5), (1, 16, 2), (3, 32, 2)])
+def test_shapes(device, heads, head_dim, layers):
+    _run_case(device, heads=heads, head_dim=head_dim, layers=layers, moved=64, seed=5)
+
+
+def test_skip_unmapped_and_same_position(device):
+    _run_case(device, skip_unmapped=True, same_every=3, seed=6)
+
+
+def test_misaligned_and_strided_layers(device):
+    _run_case(device, misalign=True, seed=7)  # element-wise path inside the vector kernel
+    _run_case(device, slot_stride_extra=8, seed=8)
+    _run_case(device, slot_stride_extra=3, seed=9)  # generic kernel (odd stride)
+
+
+def test_odd_rotary_goes_generic(device):
+    _run_case(device, head_dim=40, rotary_dim=10, seed=10, table_kind="plain")
+
+
+def test_tiny_workload_bit_exact(device):
+    case = single_request("tiny", device)
+    w = case["workload"]
+    pool = synth.make_pool(w.model, w.pool_slots, device, seed=0, generate_on_device=False)
+    table = synth.rope_table(w, device)
+    k_np = [to_storage(t) for t in pool.k]
+    v_np = [to_storage(t) for t in pool.v]
+    rp.reposition_kv_layers(k_np, v_np, case["src"].cpu().numpy(), case["dst"].cpu().numpy(),
+                            case["pairs"].cpu().numpy(), to_storage(table), dtype="bf16")
+    ops.reposition_kv_layers(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], case["src"], case["dst"],
+                             case["pairs"], table)
+    torch.cuda.synchronize()
+    for l in range(w.model.n_layers):
+        assert storage_equal(to_storage(pool.k[l]), k_np[l])
+        assert storage_equal(to_storage(pool.v[l]), v_np[l])
+
+
+def test_gpt_oss_32k_full_size(device):
+    case = single_request("gpt-oss-32k", device)
+    w = case["workload"]
+    pool = synth.make_pool(w.model, w.pool_slots, device, seed=0)
+    table = synth.rope_table(w, device)
+    src, dst, pairs = case["src"], case["dst"], case["pairs"]
+    # rows of a sample of moved tokens, before the Reposition
+    rng = np.random.default_rng(0)
+    sample = np.sort(rng.choice(len(src), size=64, replace=False))
+    s_src = src[sample].long()
+    before_k = [t[s_src].cpu() for t in pool.k]
+    before_v = [t[s_src].cpu() for t in pool.v]
+    # checksum of everything but the destination rows
+    mask = torch.ones(w.pool_slots, dtype=torch.bool, device=device)
+    mask[dst.long()] = False
+    keep_sum = [t[mask].view(torch.int16).to(torch.int64).sum().item() for t in pool.k + pool.v]
+    ops.reposition_kv_layers(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], src, dst, pairs, table)
+    torch.cuda.synchronize()
+    # V moved bit for bit for every token and layer
+    for t in pool.v:
+        assert torch.equal(t[dst.long()].view(torch.int16), t[src.long()].view(torch.int16))
+    # nothing outside the destinations changed
+    after_sum = [t[mask].view(torch.int16).to(torch.int64).sum().item() for t in pool.k + pool.v]
+    assert after_sum == keep_sum
+    # sampled oracle check of K across all 36 layers
+    s_dst = dst[sample].long()
+    table_np = to_storage(table)
+    s_pairs = pairs[sample].cpu().numpy()
+    for l in range(w.model.n_layers):
+        k_rows = [to_storage(before_k[l])]
+        v_rows = [to_storage(before_v[l])]
+        n = len(sample)
+        kk = [np.concatenate((k_rows[0], np.zeros_like(k_rows[0])))]
+        vv = [np.concatenate((v_rows[0], np.zeros_like(v_rows[0])))]
+        rp.reposition_kv_layers(kk, vv, np.arange(n), np.arange(n, 2 * n), s_pairs, table_np, dtype="bf16")
+        got = to_storage(pool.k[l][s_dst])
+        assert storage_equal(got, kk[0][n:]), f"layer {l}"
+
+
+def test_validation_messages(device):
+    k = torch.zeros((8, 2, 64), dtype=torch.bfloat16, device=device)
+    ptr = torch.tensor([k.data_ptr()], dtype=torch.uint64, device=device)
+    s = torch.zeros(1, dtype=torch.int32, device=device)
+    p = torch.zeros((1, 2), dtype=torch.int32, device=device)
+    t = torch.zeros((4, 64), dtype=torch.float32, device=device)
+    ok = dict(k_data_ptrs=ptr, v_data_ptrs=ptr, k_layout=k, v_layout=k, source_slots=s,
+              destination_slots=s, position_pairs=p, cos_sin_cache=t)
+    cases = [
+        (dict(k_layout=k.to(torch.int8)), "Context Reposition requires unquantized floating-point KV"),
+        (dict(v_layout=k[:, :1]), "Reposition requires matching native NHD K/V layouts"),
+        (dict(k_layout=k.transpose(1, 2).contiguous().transpose(1, 2), v_layout=k.transpose(1, 2).contiguous().transpose(1, 2)),
+         "Reposition requires contiguous head dimensions"),
+        (dict(k_data_ptrs=ptr.to(torch.int32)), "Reposition requires contiguous 64-bit layer pointer tables"),
+        (dict(source_slots=s.long()), "Reposition requires int32 slot vectors and [N, 2] positions"),
+        (dict(position_pairs=p[:, :1]), "Reposition requires int32 slot vectors and [N, 2] positions"),
+        (dict(cos_sin_cache=t[:, :32]), "Reposition requires a native cos/sin cache matching rotary_dim"),
+        (dict(cos_sin_cache=t.cpu()), "Reposition tensors must be on one CUDA device"),
+    ]
+    for change, message in cases:
+        args = dict(ok)
+        args.update(change)
+        with pytest.raises(ValueError, match=re.escape(message)):
+            ops.reposition_kv_layers(**args)
+    with pytest.raises(ValueError, match="Context Reposition requires page_size=1"):
+        ops.reposition_kv_layers(**ok, page_size=16)
+    # empty work returns without a launch
+    ops.reposition_kv_layers(**dict(ok, source_slots=s[:0], destination_slots=s[:0], position_pairs=p[:0]))
