@@ -30,7 +30,7 @@ _SIGNATURES = {
     "akv_compact_workspace_bytes": (c_int64, [c_int32, c_int64]),
     "akv_compact_rows": (
         c_int32,
-        [c_int32, _P, c_int64, _P, c_int64, _P, _P, _P, _P, _P, _P, c_int64, _P, c_int64,
+        [c_int32, _P, c_int64, _P, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, c_int64,
          _P, _P, _P, _P, _P, c_int64, _P, _P, c_int64, _P, _P, _P, c_int64, _P, _P],
     ),
     "akv_decode_indices": (

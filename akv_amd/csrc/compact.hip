@@ -11,7 +11,9 @@
 // (akv/system/sglang/srt/disaggregation/context_transfer.py:110-128).
 //
 // Three launches, no inter-workgroup waiting:
-//   1. count:   tiles of kTile tokens per request; wave ballots + popcount,
+//   1. count:   tiles of 256 x steps tokens per request (steps grows with the
+//               batch so a single request still spreads over many
+//               workgroups); wave ballots + popcount,
 //               wave totals through LDS -> per-tile (kept, moved)
 //   2. offsets: one workgroup scans the tile counts in request-major order
 //               -> flat output offsets per tile, per-request counts, kv_indptr
@@ -24,8 +26,20 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kSteps = 16;
-constexpr int kTile = kThreads * kSteps;  // 4096 tokens per workgroup
+constexpr int kMaxSteps = 16;  // at most 4096 tokens per workgroup
+
+// Steps of 256 tokens per tile: about 1024 tiles over the whole batch.
+int tile_steps(int32_t n_requests, int64_t max_tokens) {
+  const int64_t work = static_cast<int64_t>(n_requests) * max_tokens;
+  int steps = 1;
+  while (steps < kMaxSteps && work > static_cast<int64_t>(kThreads) * steps * 1024) steps <<= 1;
+  return steps;
+}
+
+int64_t tiles_per_request(int32_t n_requests, int64_t max_tokens) {
+  const int64_t tile = static_cast<int64_t>(kThreads) * tile_steps(n_requests, max_tokens);
+  return max_tokens <= 0 ? 1 : (max_tokens + tile - 1) / tile;
+}
 
 struct CompactArgs {
   const int64_t* req_offsets;
@@ -36,6 +50,7 @@ struct CompactArgs {
   const uint8_t* keep;
   const int32_t* birth;
   const int32_t* final_pos;
+  const int32_t* birth_slots;  // flat birth slots, or nullptr: read the row
   const int32_t* fresh;
   int64_t fresh_count;
   int32_t* retired;
@@ -59,6 +74,7 @@ struct CompactArgs {
   int64_t* req_kept;       // [B] kept tokens per request
   int32_t n_requests;
   int32_t tiles_per_req;
+  int32_t steps;  // 256-token steps per tile
 };
 
 __device__ __forceinline__ int32_t* request_row(const CompactArgs& a, int b) {
@@ -80,11 +96,11 @@ __global__ void __launch_bounds__(kThreads) compact_count_kernel(const CompactAr
   const int tile = blockIdx.x;
   const int64_t base = a.req_offsets[b];
   const int64_t n = a.req_offsets[b + 1] - base;
-  const int64_t start = static_cast<int64_t>(tile) * kTile;
+  const int64_t start = static_cast<int64_t>(tile) * kThreads * a.steps;
   __shared__ int wave_sums[2][kWaves];
   int kept = 0, moved = 0;
   if (start < n) {
-    for (int s = 0; s < kSteps; ++s) {
+    for (int s = 0; s < a.steps; ++s) {
       const int64_t i = start + s * kThreads + threadIdx.x;
       if (i < n) {
         const bool k = a.keep[base + i] != 0;
@@ -130,8 +146,9 @@ __global__ void __launch_bounds__(1024) compact_offsets_kernel(const CompactArgs
       const int b = static_cast<int>(e / a.tiles_per_req);
       const int t = static_cast<int>(e - static_cast<int64_t>(b) * a.tiles_per_req);
       const int64_t n = a.req_offsets[b + 1] - a.req_offsets[b];
-      const int64_t len = n - static_cast<int64_t>(t) * kTile;
-      const int64_t tile_len = len <= 0 ? 0 : (len < kTile ? len : kTile);
+      const int64_t tile = static_cast<int64_t>(kThreads) * a.steps;
+      const int64_t len = n - static_cast<int64_t>(t) * tile;
+      const int64_t tile_len = len <= 0 ? 0 : (len < tile ? len : tile);
       v[0] = a.tile_counts[2 * e];
       v[1] = a.tile_counts[2 * e + 1];
       v[2] = tile_len - v[0] + v[1];
@@ -230,7 +247,7 @@ __global__ void __launch_bounds__(kThreads) compact_scatter_kernel(const Compact
   const int tile = blockIdx.x;
   const int64_t base = a.req_offsets[b];
   const int64_t n = a.req_offsets[b + 1] - base;
-  const int64_t start = static_cast<int64_t>(tile) * kTile;
+  const int64_t start = static_cast<int64_t>(tile) * kThreads * a.steps;
   int32_t* row = request_row(a, b);
   const int64_t kv_base = a.req_kv_base[b];
   const int64_t req_kept_base = a.tile_offsets[3 * (static_cast<int64_t>(b) * a.tiles_per_req)];
@@ -250,7 +267,7 @@ __global__ void __launch_bounds__(kThreads) compact_scatter_kernel(const Compact
   const int64_t* toff = a.tile_offsets + 3 * (static_cast<int64_t>(b) * a.tiles_per_req + tile);
   int64_t carry_kept = toff[0], carry_moved = toff[1], carry_retired = toff[2];
   const int w = threadIdx.x >> 6;
-  for (int s = 0; s < kSteps; ++s) {
+  for (int s = 0; s < a.steps; ++s) {
     const int64_t i = start + s * kThreads + threadIdx.x;
     const bool valid = i < n;
     bool kept = false, moved = false;
@@ -260,7 +277,7 @@ __global__ void __launch_bounds__(kThreads) compact_scatter_kernel(const Compact
       bpos = a.birth[base + i];
       fpos = a.final_pos[base + i];
       moved = kept && bpos != fpos;
-      slot = row[i];
+      slot = a.birth_slots ? a.birth_slots[base + i] : row[i];
     }
     const bool retired = valid && (!kept || moved);
     const uint64_t mk = __ballot(kept);
@@ -326,7 +343,7 @@ __global__ void __launch_bounds__(kThreads) compact_scatter_kernel(const Compact
 extern "C" int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t max_tokens) {
   using namespace akv;
   if (n_requests < 0 || max_tokens < 0) return -1;
-  const int64_t tiles = max_tokens <= 0 ? 1 : (max_tokens + kTile - 1) / kTile;
+  const int64_t tiles = tiles_per_request(n_requests, max_tokens);
   const int64_t entries = static_cast<int64_t>(n_requests) * tiles;
   // int64 sections first (8-byte aligned), then the int32 tile counts
   return entries * 3 * 8 + static_cast<int64_t>(n_requests) * 16 + entries * 2 * 4;
@@ -336,7 +353,7 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
                                 int32_t* table, int64_t row_stride, const int64_t* row_pointers,
                                 const int64_t* req_rows, const uint8_t* keep,
                                 const int32_t* birth_positions, const int32_t* final_positions,
-                                const int32_t* fresh_slots, int64_t fresh_count, int32_t* retired,
+                                const int32_t* birth_slots, const int32_t* fresh_slots, int64_t fresh_count, int32_t* retired,
                                 int64_t retired_capacity, int32_t* copy_src, int32_t* copy_dst,
                                 int32_t* copy_pairs, int32_t* raw_indices,
                                 int32_t* active_positions, int64_t kept_capacity,
@@ -362,7 +379,7 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
                 static_cast<long long>(workspace_bytes), static_cast<long long>(need));
   if ((reinterpret_cast<uintptr_t>(workspace) & 7) != 0)
     return fail(AKV_EINVAL, "akv_compact_rows: workspace must be 8-byte aligned");
-  const int64_t tiles = max_tokens <= 0 ? 1 : (max_tokens + kTile - 1) / kTile;
+  const int64_t tiles = tiles_per_request(n_requests, max_tokens);
   if (tiles > 65535 || n_requests > 65535)
     return fail(AKV_EINVAL, "akv_compact_rows: batch too large (%d requests, %lld tiles)", n_requests,
                 static_cast<long long>(tiles));
@@ -377,6 +394,7 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
   a.keep = keep;
   a.birth = birth_positions;
   a.final_pos = final_positions;
+  a.birth_slots = birth_slots;
   a.fresh = fresh_slots;
   a.fresh_count = fresh_count;
   a.retired = retired;
@@ -400,6 +418,7 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
   a.tile_counts = reinterpret_cast<int32_t*>(ws + entries * 3 * 8 + static_cast<int64_t>(n_requests) * 16);
   a.n_requests = n_requests;
   a.tiles_per_req = static_cast<int32_t>(tiles);
+  a.steps = tile_steps(n_requests, max_tokens);
 
   hipStream_t st = as_stream(stream);
   const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(n_requests));

@@ -41,7 +41,9 @@ struct RepositionArgs {
   int32_t is_neox;
   int32_t units_per_head;  // rotary units per head
   int32_t lanes_per_row;   // n_heads * units_per_head
-  int32_t rows_per_block;  // layers processed side by side by one workgroup
+  int32_t rows_per_block;  // layers processed side by side by one token
+  int32_t tokens_per_block;
+  int64_t n_tokens;
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -155,11 +157,16 @@ __device__ __forceinline__ u32x4 pack<float>(const float (&f)[4]) {
 // instructions.
 typedef __attribute__((address_space(1))) u32x4 global_u32x4;
 
-// 16-byte load/store; `aligned` is wave-uniform.  The KV rows are touched
-// exactly once per Reposition, so they bypass the caches' reuse policy.
+// 16-byte load/store; `aligned` is wave-uniform.  Plain (temporal) accesses:
+// on MI355X they measured faster than the nontemporal forms for this
+// scattered 1 KiB-row pattern (AKV_REPOSITION_NT selects the latter).
 template <typename T>
 __device__ __forceinline__ u32x4 load16(const T* p, bool aligned) {
+#ifdef AKV_REPOSITION_NT
   if (aligned) return __builtin_nontemporal_load((const global_u32x4*)(p));
+#else
+  if (aligned) return *((const global_u32x4*)(p));
+#endif
   union {
     u32x4 u;
     T e[Elem<T>::kVec];
@@ -172,7 +179,11 @@ __device__ __forceinline__ u32x4 load16(const T* p, bool aligned) {
 template <typename T>
 __device__ __forceinline__ void store16(T* p, u32x4 v, bool aligned) {
   if (aligned) {
+#ifdef AKV_REPOSITION_NT
     __builtin_nontemporal_store(v, (global_u32x4*)(p));
+#else
+    *((global_u32x4*)(p)) = v;
+#endif
     return;
   }
   union {
@@ -204,86 +215,56 @@ __device__ __forceinline__ void rotate(float x1, float x2, float co, float so, f
   y2 = u2 * cn + u1 * sn;
 }
 
+// Registers of one (token, layer) row between its loads and its stores.
+struct RowData {
+  u32x4 k1, k2;  // rotary unit of K (the partner half for NeoX style)
+  u32x4 v[2];    // this lane's first two V units
+  uintptr_t kb, vb;
+  bool aligned;
+};
+
 template <typename T, typename CS, bool NEOX>
-__global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionArgs a) {
-  constexpr int VEC = Elem<T>::kVec;
-  constexpr int NP = NEOX ? VEC : VEC / 2;  // rotation pairs per lane
-  const int lpr = a.lanes_per_row;
-  const int row_sub = threadIdx.x / lpr;
-  const int j = threadIdx.x - row_sub * lpr;
-  if (row_sub >= a.rows_per_block) return;
-
-  const int64_t token = blockIdx.x;
-  const int64_t src = a.src[token];
-  const int64_t dst = a.dst[token];
-  if (a.skip_unmapped && (src <= 0 || dst <= 0)) return;
-  const int32_t* pair = a.pairs + token * a.pair_stride;
-  const int64_t old_pos = pair[0];
-  const int64_t new_pos = pair[1];
-  const bool same = old_pos == new_pos;
-
-  const int R = a.rotary_dim;
-  const int half = R >> 1;
-  const int D = a.head_dim;
-  const int h = j / a.units_per_head;
-  const int g = j - h * a.units_per_head;
-  // element offsets (within a head) of this lane's rotary unit
-  const int off1 = g * VEC;
-  const int off2 = NEOX ? half + g * VEC : 0;
-  const int i0 = NEOX ? g * VEC : g * (VEC / 2);
-
+struct RowMover {
+  static constexpr int VEC = Elem<T>::kVec;
+  static constexpr int NP = NEOX ? VEC : VEC / 2;  // rotation pairs per lane
+  const RepositionArgs& a;
+  int64_t src, dst;
+  int h, j, off1, off2, lpr, v_units_head, v_units_row, t_units_head, t_units_row;
+  bool same;
   float co[NP], so[NP], cn[NP], sn[NP], s2[NP];
-  if (!same) {
-    const CS* table = static_cast<const CS*>(a.cos_sin);
-    load_table<CS, NP>(table + old_pos * a.rope_stride + i0, co);
-    load_table<CS, NP>(table + old_pos * a.rope_stride + half + i0, so);
-    load_table<CS, NP>(table + new_pos * a.rope_stride + i0, cn);
-    load_table<CS, NP>(table + new_pos * a.rope_stride + half + i0, sn);
-#pragma unroll
-    for (int k = 0; k < NP; ++k) s2[k] = co[k] * co[k] + so[k] * so[k];
-  }
 
-  const int v_units_head = D / VEC;
-  const int v_units_row = a.n_heads * v_units_head;
-  const int t_units_head = (D - R) / VEC;
-  const int t_units_row = a.n_heads * t_units_head;
-
-  for (int layer = row_sub; layer < a.n_layers; layer += a.rows_per_block) {
-    T* kb = reinterpret_cast<T*>(a.k_ptrs[layer]);
-    T* vb = reinterpret_cast<T*>(a.v_ptrs[layer]);
-    // one wave may hold rows of two layers: take the vector path only when
-    // every row of the wave is 16-byte aligned (a scalar, uniform branch)
-    const bool lane_aligned =
-        ((reinterpret_cast<uintptr_t>(kb) | reinterpret_cast<uintptr_t>(vb)) & 15) == 0;
-    const bool aligned = __ballot(!lane_aligned) == 0;
-    const T* ks = kb + src * a.k_stride_slot + h * a.k_stride_head;
-    T* kd = kb + dst * a.k_stride_slot + h * a.k_stride_head;
-
-    // ---- rotary part of K
-    const u32x4 r1 = load16(ks + off1, aligned);
-    u32x4 r2 = make_u32x4(0, 0, 0, 0);
-    if (NEOX) r2 = load16(ks + off2, aligned);
-    // ---- V (and the non-rotary K tail), issued before the arithmetic
-    const T* vs = vb + src * a.v_stride_slot;
-    T* vd = vb + dst * a.v_stride_slot;
-    u32x4 vv[2];
-    int vc[2];
+  __device__ __forceinline__ RowData load(int layer) const {
+    RowData r;
+    r.kb = static_cast<uintptr_t>(a.k_ptrs[layer]);
+    r.vb = static_cast<uintptr_t>(a.v_ptrs[layer]);
+    // one wave may hold rows of several layers: take the vector path only
+    // when every row of the wave is 16-byte aligned (a uniform branch)
+    r.aligned = __ballot(((r.kb | r.vb) & 15) != 0) == 0;
+    const T* ks = reinterpret_cast<const T*>(r.kb) + src * a.k_stride_slot + h * a.k_stride_head;
+    r.k1 = load16(ks + off1, r.aligned);
+    r.k2 = NEOX ? load16(ks + off2, r.aligned) : make_u32x4(0, 0, 0, 0);
+    const T* vs = reinterpret_cast<const T*>(r.vb) + src * a.v_stride_slot;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      vc[q] = j + q * lpr;
-      if (vc[q] < v_units_row) {
-        const int vh = vc[q] / v_units_head;
-        const int ve = (vc[q] - vh * v_units_head) * VEC;
-        vv[q] = load16(vs + vh * a.v_stride_head + ve, aligned);
+      const int c = j + q * lpr;
+      if (c < v_units_row) {
+        const int vh = c / v_units_head;
+        r.v[q] = load16(vs + vh * a.v_stride_head + (c - vh * v_units_head) * VEC, r.aligned);
       }
     }
+    return r;
+  }
 
-    u32x4 o1 = r1, o2 = r2;
+  __device__ __forceinline__ void finish(const RowData& r) const {
+    T* kb = reinterpret_cast<T*>(r.kb);
+    T* vb = reinterpret_cast<T*>(r.vb);
+    T* kd = kb + dst * a.k_stride_slot + h * a.k_stride_head;
+    u32x4 o1 = r.k1, o2 = r.k2;
     if (!same) {
       float x1[VEC], x2[VEC], y1[VEC], y2[VEC];
-      unpack<T>(r1, x1);
+      unpack<T>(r.k1, x1);
       if (NEOX) {
-        unpack<T>(r2, x2);
+        unpack<T>(r.k2, x2);
 #pragma unroll
         for (int k = 0; k < NP; ++k) rotate(x1[k], x2[k], co[k], so[k], s2[k], cn[k], sn[k], y1[k], y2[k]);
         o1 = pack<T>(y1);
@@ -295,30 +276,91 @@ __global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionAr
         o1 = pack<T>(y1);
       }
     }
-    store16(kd + off1, o1, aligned);
-    if (NEOX) store16(kd + off2, o2, aligned);
-
+    store16(kd + off1, o1, r.aligned);
+    if (NEOX) store16(kd + off2, o2, r.aligned);
+    const T* vs = vb + src * a.v_stride_slot;
+    T* vd = vb + dst * a.v_stride_slot;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      if (vc[q] < v_units_row) {
-        const int vh = vc[q] / v_units_head;
-        const int ve = (vc[q] - vh * v_units_head) * VEC;
-        store16(vd + vh * a.v_stride_head + ve, vv[q], aligned);
+      const int c = j + q * lpr;
+      if (c < v_units_row) {
+        const int vh = c / v_units_head;
+        store16(vd + vh * a.v_stride_head + (c - vh * v_units_head) * VEC, r.v[q], r.aligned);
       }
     }
     // V units beyond two per lane (wide heads with few rotary units)
     for (int c = j + 2 * lpr; c < v_units_row; c += lpr) {
       const int vh = c / v_units_head;
       const int ve = (c - vh * v_units_head) * VEC;
-      store16(vd + vh * a.v_stride_head + ve, load16(vs + vh * a.v_stride_head + ve, aligned), aligned);
+      store16(vd + vh * a.v_stride_head + ve, load16(vs + vh * a.v_stride_head + ve, r.aligned), r.aligned);
     }
     // K tail dims [R, D)
     for (int c = j; c < t_units_row; c += lpr) {
       const int th = c / t_units_head;
-      const int te = R + (c - th * t_units_head) * VEC;
+      const int te = a.rotary_dim + (c - th * t_units_head) * VEC;
       const T* ts = kb + src * a.k_stride_slot + th * a.k_stride_head + te;
       T* td = kb + dst * a.k_stride_slot + th * a.k_stride_head + te;
-      store16(td, load16(ts, aligned), aligned);
+      store16(td, load16(ts, r.aligned), r.aligned);
+    }
+  }
+};
+
+// Workgroup = tokens_per_block tokens x rows_per_block layer rows side by
+// side x lanes_per_row lanes; each lane walks the layers of its token.
+template <typename T, typename CS, bool NEOX>
+__global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionArgs a) {
+  using Mover = RowMover<T, CS, NEOX>;
+  constexpr int VEC = Mover::VEC;
+  constexpr int NP = Mover::NP;
+  const int lpr = a.lanes_per_row;
+  const int row_threads = lpr * a.rows_per_block;
+  const int slot = threadIdx.x / row_threads;
+  const int local = threadIdx.x - slot * row_threads;
+  const int row_sub = local / lpr;
+  const int j = local - row_sub * lpr;
+  const int64_t token = static_cast<int64_t>(blockIdx.x) * a.tokens_per_block + slot;
+  if (slot >= a.tokens_per_block || token >= a.n_tokens) return;
+
+  Mover mv{a};
+  mv.src = a.src[token];
+  mv.dst = a.dst[token];
+  if (a.skip_unmapped && (mv.src <= 0 || mv.dst <= 0)) return;
+  const int32_t* pair = a.pairs + token * a.pair_stride;
+  const int64_t old_pos = pair[0];
+  const int64_t new_pos = pair[1];
+  mv.same = old_pos == new_pos;
+  const int half = a.rotary_dim >> 1;
+  mv.lpr = lpr;
+  mv.j = j;
+  mv.h = j / a.units_per_head;
+  const int g = j - mv.h * a.units_per_head;
+  mv.off1 = g * VEC;
+  mv.off2 = NEOX ? half + g * VEC : 0;
+  const int i0 = NEOX ? g * VEC : g * (VEC / 2);
+  mv.v_units_head = a.head_dim / VEC;
+  mv.v_units_row = a.n_heads * mv.v_units_head;
+  mv.t_units_head = (a.head_dim - a.rotary_dim) / VEC;
+  mv.t_units_row = a.n_heads * mv.t_units_head;
+  if (!mv.same) {
+    const CS* table = static_cast<const CS*>(a.cos_sin);
+    load_table<CS, NP>(table + old_pos * a.rope_stride + i0, mv.co);
+    load_table<CS, NP>(table + old_pos * a.rope_stride + half + i0, mv.so);
+    load_table<CS, NP>(table + new_pos * a.rope_stride + i0, mv.cn);
+    load_table<CS, NP>(table + new_pos * a.rope_stride + half + i0, mv.sn);
+#pragma unroll
+    for (int k = 0; k < NP; ++k) mv.s2[k] = mv.co[k] * mv.co[k] + mv.so[k] * mv.so[k];
+  }
+
+  // Double-buffered over layers: the next row's loads are in flight during
+  // this row's arithmetic and stores (measured +2% over load-then-finish).
+  if (row_sub < a.n_layers) {
+    RowData cur = mv.load(row_sub);
+    for (int layer = row_sub; layer < a.n_layers; layer += a.rows_per_block) {
+      const int next = layer + a.rows_per_block;
+      RowData nxt = cur;
+      if (next < a.n_layers) nxt = mv.load(next);
+      mv.finish(cur);
+      cur = nxt;
     }
   }
 }
@@ -376,31 +418,45 @@ __global__ void __launch_bounds__(256) reposition_generic_kernel(const Repositio
   }
 }
 
-int rows_per_block_for(int lanes_per_row, int n_layers) {
-  static const int forced = [] {
-    const char* e = std::getenv("AKV_REPOSITION_ROWS_PER_BLOCK");
-    return e ? std::atoi(e) : 0;
-  }();
-  int rpb = forced > 0 ? forced : 512 / lanes_per_row;
-  if (rpb < 1) rpb = 1;
-  if (rpb > n_layers) rpb = n_layers;
-  if (forced <= 0) {
-    const int passes = (n_layers + rpb - 1) / rpb;
-    rpb = (n_layers + passes - 1) / passes;  // balance the passes
+int env_int(const char* name) {
+  const char* e = std::getenv(name);
+  return e ? std::atoi(e) : 0;
+}
+
+// Launch geometry of the vector kernel.  Measured on MI355X for the
+// 36-layer x 8-head x 64 bf16 shape: about 192 threads per token (6 layers
+// side by side, 6 passes each) beat both one wave per token and one row per
+// lane; tokens whose rows fill less than two waves share a workgroup.
+// AKV_REPOSITION_ROWS_PER_BLOCK / AKV_REPOSITION_TOKENS_PER_BLOCK override.
+void geometry(RepositionArgs& a) {
+  const int lpr = a.lanes_per_row;
+  const int forced_rows = env_int("AKV_REPOSITION_ROWS_PER_BLOCK");
+  int rows = forced_rows > 0 ? forced_rows : 192 / lpr;
+  if (rows < 1) rows = 1;
+  if (rows > a.n_layers) rows = a.n_layers;
+  if (forced_rows <= 0) {
+    const int passes = (a.n_layers + rows - 1) / rows;
+    rows = (a.n_layers + passes - 1) / passes;  // balance the passes
   }
-  while (rpb > 1 && rpb * lanes_per_row > 1024) --rpb;
-  return rpb;
+  while (rows > 1 && rows * lpr > 1024) --rows;
+  a.rows_per_block = rows;
+  const int forced_tokens = env_int("AKV_REPOSITION_TOKENS_PER_BLOCK");
+  int tokens = forced_tokens > 0 ? forced_tokens : 128 / (rows * lpr);
+  if (tokens < 1) tokens = 1;
+  while (tokens > 1 && tokens * rows * lpr > 1024) --tokens;
+  a.tokens_per_block = tokens;
 }
 
 template <typename T, typename CS>
 int launch_typed(RepositionArgs a, int64_t n_tokens, hipStream_t stream, bool vec_ok) {
   constexpr int VEC = Elem<T>::kVec;
+  a.n_tokens = n_tokens;
   if (vec_ok) {
     a.units_per_head = a.is_neox ? a.rotary_dim / (2 * VEC) : a.rotary_dim / VEC;
     a.lanes_per_row = a.n_heads * a.units_per_head;
-    a.rows_per_block = rows_per_block_for(a.lanes_per_row, a.n_layers);
-    const int threads = a.lanes_per_row * a.rows_per_block;
-    const dim3 grid(static_cast<unsigned>(n_tokens));
+    geometry(a);
+    const int threads = a.lanes_per_row * a.rows_per_block * a.tokens_per_block;
+    const dim3 grid(static_cast<unsigned>((n_tokens + a.tokens_per_block - 1) / a.tokens_per_block));
     if (a.is_neox)
       hipLaunchKernelGGL((reposition_vec_kernel<T, CS, true>), grid, dim3(threads), 0, stream, a);
     else

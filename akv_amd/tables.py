@@ -143,7 +143,7 @@ def allocate_outputs(inputs, device, *, generated_total=None):
 
 
 def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_pointers=None,
-                 generated=None):
+                 generated=None, birth_slots=None):
     """Rewrite each request's raw row to its terminal form and emit the lists.
 
     ``req_to_token``: int32 ``[pool_rows, width]`` request table (rows hold the
@@ -152,6 +152,9 @@ def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_po
     moved tokens.  ``row_pointers``: optional int64 ``[pool_rows]`` side-row
     table (``RowPointers``, ``akv/system/sglang.patch:242-278``).  ``generated``:
     optional int32 ``[B]`` count of generated entries to append per request.
+    ``birth_slots``: optional int32 flat birth slots (request-major, like the
+    keep mask); when given the raw rows are only written, never read, so the
+    call can be repeated on the same inputs.
     """
     if req_to_token.dtype != torch.int32 or req_to_token.ndim != 2 or req_to_token.stride(1) != 1:
         raise ValueError("req_to_token must be an int32 [rows, width] table with unit column stride")
@@ -163,6 +166,9 @@ def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_po
         raise ValueError("row_pointers must be int64 addresses")
     if generated is not None and (generated.dtype != torch.int32 or generated.shape != (inputs.n_requests,)):
         raise ValueError("generated must be int32 [B]")
+    if birth_slots is not None and (birth_slots.dtype != torch.int32
+                                    or birth_slots.shape != (sum(inputs.n_tokens),)):
+        raise ValueError("birth_slots must be int32 with one slot per raw token")
     if generated is not None and outputs.kv_indices is None:
         raise ValueError("generated entries need kv_indices outputs")
     lib = _lib.load()
@@ -179,6 +185,7 @@ def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_po
             inputs.keep.data_ptr(),
             inputs.birth_positions.data_ptr(),
             inputs.final_positions.data_ptr(),
+            _lib.ptr(birth_slots),
             _lib.ptr(fresh_slots) if inputs.moved_total else None,
             inputs.moved_total,
             outputs.retired.data_ptr(),

@@ -78,9 +78,11 @@ int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t max_tokens);
  * request b, raw tokens [req_offsets[b], req_offsets[b+1]) of the flat
  * keep / birth_positions / final_positions vectors; its raw row is
  * row_pointers[req_rows[b]] when row_pointers != NULL, else
- * table + req_rows[b] * row_stride, and holds the birth slots on entry.
- * A kept token is "moved" when its final position differs from its birth
- * position; moved tokens take fresh_slots in request-major raw order.
+ * table + req_rows[b] * row_stride.  The birth slots are read from the flat
+ * birth_slots vector (same indexing as keep) when it is not NULL, else from
+ * the raw row itself (which then holds them on entry).  A kept token is
+ * "moved" when its final position differs from its birth position; moved
+ * tokens take fresh_slots in request-major raw order.
  * Outputs (flat, request-major, raw order):
  *   raw row (in place)  keep ? (moved ? fresh : birth) : -1
  *   retired             birth slots of dropped or moved tokens
@@ -102,7 +104,8 @@ int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets,
                      int64_t max_tokens, int32_t* table, int64_t row_stride,
                      const int64_t* row_pointers, const int64_t* req_rows,
                      const uint8_t* keep, const int32_t* birth_positions,
-                     const int32_t* final_positions, const int32_t* fresh_slots,
+                     const int32_t* final_positions, const int32_t* birth_slots,
+                     const int32_t* fresh_slots,
                      int64_t fresh_count, int32_t* retired,
                      int64_t retired_capacity, int32_t* copy_src,
                      int32_t* copy_dst, int32_t* copy_pairs,

@@ -120,6 +120,22 @@ def test_side_rows_and_edge_requests(device):
     _run(device, w, side_rows=True, generated=[2, 0, 1, 3, 1, 0])
 
 
+def test_birth_slot_vector_is_idempotent(device):
+    w = synth.workload("ragged-64")
+    layouts = synth.compile_layouts(w)
+    slots, inputs, table, req_rows, fresh, row_pointers, side, tails = _setup(device, w, layouts)
+    birth = torch.from_numpy(np.concatenate(slots.birth_rows)).to(device)
+    # rows start out as garbage: with a birth vector they are only written
+    table.fill_(-77)
+    out = tables.allocate_outputs(inputs, device, generated_total=0)
+    gen0 = torch.zeros(w.n_requests, dtype=torch.int32, device=device)
+    for _ in range(2):
+        tables.compact_rows(inputs, table, req_rows, fresh, out, generated=gen0, birth_slots=birth)
+    torch.cuda.synchronize()
+    rows_after = [table[r].cpu().numpy() for r in req_rows.cpu().numpy()]
+    _check(w, layouts, slots, out, rows_after, [np.zeros(0, np.int32)] * w.n_requests, [0] * w.n_requests)
+
+
 def test_fresh_count_mismatch_sets_status(device):
     w = synth.workload("tiny")
     layouts = synth.compile_layouts(w)
