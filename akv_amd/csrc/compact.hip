@@ -10,13 +10,16 @@
 // active row of request_active_slots
 // (akv/system/sglang/srt/disaggregation/context_transfer.py:110-128).
 //
-// Three launches, no inter-workgroup waiting:
+// Two or three launches, no inter-workgroup waiting:
 //   1. count:   tiles of 256 x steps tokens per request (steps grows with the
 //               batch so a single request still spreads over many
 //               workgroups); wave ballots + popcount,
 //               wave totals through LDS -> per-tile (kept, moved)
-//   2. offsets: one workgroup scans the tile counts in request-major order
-//               -> flat output offsets per tile, per-request counts, kv_indptr
+//   2. offsets: (batches of more than kFusedMaxEntries tiles only) one
+//               workgroup scans the tile counts in request-major order ->
+//               flat output offsets per tile, per-request counts, kv_indptr;
+//               smaller batches derive these inside the scatter workgroups
+//               from a block reduction over the earlier tiles' counts
 //   3. scatter: same tiles again; ballot/mbcnt ranks inside each 256-token
 //               step, LDS wave totals, running carry -> every output.
 #include "common.h"
@@ -27,6 +30,9 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxSteps = 16;  // at most 4096 tokens per workgroup
+// Up to this many tiles per batch, each scatter workgroup derives its own
+// offsets from the tile counts (2 launches); beyond, a scan launch does.
+constexpr int64_t kFusedMaxEntries = 4096;
 
 // Steps of 256 tokens per tile: about 1024 tiles over the whole batch.
 int tile_steps(int32_t n_requests, int64_t max_tokens) {
@@ -242,6 +248,40 @@ __global__ void __launch_bounds__(1024) compact_offsets_kernel(const CompactArgs
   }
 }
 
+// Block-wide sum of K int64 accumulators (every thread gets the totals).
+template <int K>
+__device__ __forceinline__ void block_sum(int64_t (&v)[K], int64_t (*lds)[K]) {
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    for (int off = 32; off > 0; off >>= 1) v[k] += __shfl_xor(v[k], off);
+  const int w = threadIdx.x >> 6;
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) lds[w][k] = v[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    v[k] = 0;
+    for (int q = 0; q < kWaves; ++q) v[k] += lds[q][k];
+  }
+  __syncthreads();
+}
+
+// Tokens of tile entry e (request-major) for the tile size of this launch.
+__device__ __forceinline__ int64_t tile_length(const CompactArgs& a, int64_t e) {
+  const int rb = static_cast<int>(e / a.tiles_per_req);
+  const int rt = static_cast<int>(e - static_cast<int64_t>(rb) * a.tiles_per_req);
+  const int64_t tile = static_cast<int64_t>(kThreads) * a.steps;
+  const int64_t len = a.req_offsets[rb + 1] - a.req_offsets[rb] - rt * tile;
+  return len <= 0 ? 0 : (len < tile ? len : tile);
+}
+
+// FUSED: the tile's exclusive offsets, its request's kv base and the
+// per-request outputs come from a block reduction over the tile counts of
+// the earlier tiles (small batches: saves the offsets launch).  Otherwise
+// they come from compact_offsets_kernel.
+template <bool FUSED>
 __global__ void __launch_bounds__(kThreads) compact_scatter_kernel(const CompactArgs a) {
   const int b = blockIdx.y;
   const int tile = blockIdx.x;
@@ -249,23 +289,89 @@ __global__ void __launch_bounds__(kThreads) compact_scatter_kernel(const Compact
   const int64_t n = a.req_offsets[b + 1] - base;
   const int64_t start = static_cast<int64_t>(tile) * kThreads * a.steps;
   int32_t* row = request_row(a, b);
-  const int64_t kv_base = a.req_kv_base[b];
-  const int64_t req_kept_base = a.tile_offsets[3 * (static_cast<int64_t>(b) * a.tiles_per_req)];
+  int64_t kv_base, req_kept_base, req_kept, carry_kept, carry_moved, carry_retired;
+  if (FUSED) {
+    __shared__ int64_t lds[kWaves][7];
+    const int64_t first = static_cast<int64_t>(b) * a.tiles_per_req;
+    const int64_t me = first + tile;
+    const int64_t end = first + a.tiles_per_req;
+    // 0-2: kept/moved/retired before this tile; 3: kept before the request;
+    // 4-6: kept/moved/retired of the request
+    int64_t v[7] = {0, 0, 0, 0, 0, 0, 0};
+    for (int64_t e = threadIdx.x; e < end; e += kThreads) {
+      const int64_t k = a.tile_counts[2 * e];
+      const int64_t m = a.tile_counts[2 * e + 1];
+      const int64_t r = tile_length(a, e) - k + m;
+      if (e < me) {
+        v[0] += k;
+        v[1] += m;
+        v[2] += r;
+      }
+      if (e < first) {
+        v[3] += k;
+      } else {
+        v[4] += k;
+        v[5] += m;
+        v[6] += r;
+      }
+    }
+    int64_t gen_before = 0;
+    if (a.generated)
+      for (int q = threadIdx.x; q < b; q += kThreads) gen_before += a.generated[q];
+    int64_t g[1] = {gen_before};
+    block_sum<7>(v, lds);
+    block_sum<1>(g, reinterpret_cast<int64_t(*)[1]>(&lds[0][0]));
+    carry_kept = v[0];
+    carry_moved = v[1];
+    carry_retired = v[2];
+    req_kept_base = v[3];
+    req_kept = v[4];
+    kv_base = v[3] + g[0];
+    if (tile == 0 && threadIdx.x == 0) {
+      const int64_t gen = a.generated ? a.generated[b] : 0;
+      if (a.counts) {
+        a.counts[3 * b] = static_cast<int32_t>(v[4]);
+        a.counts[3 * b + 1] = static_cast<int32_t>(v[5]);
+        a.counts[3 * b + 2] = static_cast<int32_t>(v[6]);
+      }
+      if (a.kv_indptr) {
+        if (b == 0) a.kv_indptr[0] = 0;
+        a.kv_indptr[b + 1] = static_cast<int32_t>(kv_base + v[4] + gen);
+      }
+      if (a.status && b + 1 == a.n_requests) {
+        // this block's reduction covered every tile of the batch
+        const int64_t kept_all = v[3] + v[4];
+        // moved and retired over all tiles: those before the last request
+        // are the prefix sums of its tile 0 (v[1], v[2])
+        const int64_t moved_all = v[1] + v[5];
+        const int64_t retired_all = v[2] + v[6];
+        const bool bad = moved_all != a.fresh_count || kept_all > a.kept_capacity ||
+                         retired_all > a.retired_capacity ||
+                         (a.kv_indices && kv_base + v[4] + gen > a.kv_capacity);
+        a.status[0] = bad ? 1 : 0;
+      }
+    }
+  } else {
+    kv_base = a.req_kv_base[b];
+    req_kept = a.req_kept[b];
+    req_kept_base = a.tile_offsets[3 * (static_cast<int64_t>(b) * a.tiles_per_req)];
+    const int64_t* toff = a.tile_offsets + 3 * (static_cast<int64_t>(b) * a.tiles_per_req + tile);
+    carry_kept = toff[0];
+    carry_moved = toff[1];
+    carry_retired = toff[2];
+  }
 
   // generated raw-row entries after the prompt go after the compacted row
   if (tile == 0 && a.generated && a.kv_indices) {
-    const int64_t kept_total = a.req_kept[b];
     const int32_t gen = a.generated[b];
     for (int i = threadIdx.x; i < gen; i += kThreads) {
-      const int64_t at = kv_base + kept_total + i;
+      const int64_t at = kv_base + req_kept + i;
       if (at < a.kv_capacity) a.kv_indices[at] = row[n + i];
     }
   }
   if (start >= n) return;
 
   __shared__ int wave_sums[3][kWaves];
-  const int64_t* toff = a.tile_offsets + 3 * (static_cast<int64_t>(b) * a.tiles_per_req + tile);
-  int64_t carry_kept = toff[0], carry_moved = toff[1], carry_retired = toff[2];
   const int w = threadIdx.x >> 6;
   for (int s = 0; s < a.steps; ++s) {
     const int64_t i = start + s * kThreads + threadIdx.x;
@@ -425,9 +531,13 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
   hipLaunchKernelGGL(compact_count_kernel, grid, dim3(kThreads), 0, st, a);
   int rc = check_launch("akv_compact_rows (count)");
   if (rc) return rc;
+  if (entries <= kFusedMaxEntries) {
+    hipLaunchKernelGGL(compact_scatter_kernel<true>, grid, dim3(kThreads), 0, st, a);
+    return check_launch("akv_compact_rows (scatter)");
+  }
   hipLaunchKernelGGL(compact_offsets_kernel, dim3(1), dim3(1024), 0, st, a);
   rc = check_launch("akv_compact_rows (offsets)");
   if (rc) return rc;
-  hipLaunchKernelGGL(compact_scatter_kernel, grid, dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL(compact_scatter_kernel<false>, grid, dim3(kThreads), 0, st, a);
   return check_launch("akv_compact_rows (scatter)");
 }

@@ -306,7 +306,9 @@ def main():
         "reposition_p99_ms": round(percentile(repo_ms, 99), 5),
         "reposition_steady_ms": round(float(np.mean(repo_timed_ms)), 5),
         "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
-        "kernel_launches_per_step": 1 if args.reposition_only else 4,
+        # compaction: count + scatter (one request spans 128 tiles, under the
+        # fused-offsets limit) ; Reposition: one launch for the 36-layer group
+        "kernel_launches_per_step": 1 if args.reposition_only else 3,
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),

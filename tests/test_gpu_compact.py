@@ -120,6 +120,24 @@ def test_side_rows_and_edge_requests(device):
     _run(device, w, side_rows=True, generated=[2, 0, 1, 3, 1, 0])
 
 
+def test_many_small_requests_use_the_scan_launch(device):
+    # 5000 requests -> 5000 tiles: beyond the fused-offsets limit
+    rng = np.random.default_rng(21)
+    lengths, spans = [], []
+    for _ in range(5000):
+        n = int(rng.integers(1, 40))
+        s = []
+        if n > 3 and rng.random() < 0.8:
+            a_, b_ = sorted(rng.choice(np.arange(n + 1), size=2, replace=False).tolist())
+            if b_ - a_ < n:  # a Reposition needs at least one kept token
+                s = [(a_, b_)]
+        lengths.append(n)
+        spans.append(tuple(s))
+    w = synth.Workload("many-small", synth.TINY, tuple(lengths), tuple(spans), seed=21,
+                       table_positions=64, pool_slots=4 * sum(lengths) + 1)
+    _run(device, w, generated=[int(x) for x in rng.integers(0, 3, size=len(lengths))])
+
+
 def test_birth_slot_vector_is_idempotent(device):
     w = synth.workload("ragged-64")
     layouts = synth.compile_layouts(w)
