@@ -31,7 +31,7 @@ _SIGNATURES = {
     "akv_compact_rows": (
         c_int32,
         [c_int32, _P, c_int64, _P, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, c_int64,
-         _P, _P, _P, _P, _P, c_int64, _P, _P, c_int64, _P, _P, _P, c_int64, _P, _P],
+         _P, _P, _P, _P, _P, c_int64, _P, _P, c_int64, _P, _P, c_int32, _P, _P, c_int64, _P, _P],
     ),
     "akv_decode_indices": (
         c_int32,

@@ -71,6 +71,8 @@ struct CompactArgs {
   int32_t* kv_indices;
   int64_t kv_capacity;
   int32_t* kv_indptr;
+  int32_t* last_page_len;
+  int32_t page_size;
   int32_t* counts;
   int32_t* status;
   // workspace
@@ -233,6 +235,7 @@ __global__ void __launch_bounds__(1024) compact_offsets_kernel(const CompactArgs
         if (b == 0) a.kv_indptr[0] = 0;
         a.kv_indptr[b + 1] = static_cast<int32_t>(excl + len);
       }
+      if (a.last_page_len) a.last_page_len[b] = len > 0 ? static_cast<int32_t>((len - 1) % a.page_size + 1) : 0;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -337,6 +340,10 @@ __global__ void __launch_bounds__(kThreads) compact_scatter_kernel(const Compact
       if (a.kv_indptr) {
         if (b == 0) a.kv_indptr[0] = 0;
         a.kv_indptr[b + 1] = static_cast<int32_t>(kv_base + v[4] + gen);
+      }
+      if (a.last_page_len) {
+        const int64_t len = v[4] + gen;
+        a.last_page_len[b] = len > 0 ? static_cast<int32_t>((len - 1) % a.page_size + 1) : 0;
       }
       if (a.status && b + 1 == a.n_requests) {
         // this block's reduction covered every tile of the batch
@@ -464,7 +471,8 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
                                 int32_t* copy_pairs, int32_t* raw_indices,
                                 int32_t* active_positions, int64_t kept_capacity,
                                 const int32_t* generated, int32_t* kv_indices, int64_t kv_capacity,
-                                int32_t* kv_indptr, int32_t* counts, void* workspace,
+                                int32_t* kv_indptr, int32_t* last_page_len, int32_t page_size,
+                                int32_t* counts, void* workspace,
                                 int64_t workspace_bytes, int32_t* status, void* stream) {
   using namespace akv;
   if (n_requests < 0 || max_tokens < 0)
@@ -477,6 +485,8 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
     return fail(AKV_EINVAL, "akv_compact_rows: need a request table or row pointers");
   if (fresh_count > 0 && !fresh_slots)
     return fail(AKV_EINVAL, "akv_compact_rows: fresh_count > 0 with no fresh slots");
+  if (last_page_len && page_size <= 0)
+    return fail(AKV_EINVAL, "akv_compact_rows: page_size must be positive");
   if (generated && kv_indices && !kv_indptr)
     return fail(AKV_EINVAL, "akv_compact_rows: generated tokens need kv_indptr");
   const int64_t need = akv_compact_workspace_bytes(n_requests, max_tokens);
@@ -515,6 +525,8 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
   a.kv_indices = kv_indices;
   a.kv_capacity = kv_indices ? kv_capacity : 0;
   a.kv_indptr = kv_indptr;
+  a.last_page_len = last_page_len;
+  a.page_size = page_size > 0 ? page_size : 1;
   a.counts = counts;
   a.status = status;
   char* ws = static_cast<char*>(workspace);

@@ -112,6 +112,7 @@ class CompactionOutputs:
     active_positions: torch.Tensor
     kv_indices: torch.Tensor | None
     kv_indptr: torch.Tensor | None
+    last_page_len: torch.Tensor | None
     counts: torch.Tensor
     status: torch.Tensor
     workspace: torch.Tensor
@@ -136,6 +137,7 @@ def allocate_outputs(inputs, device, *, generated_total=None):
         active_positions=torch.empty(inputs.kept_total, dtype=i32, device=device),
         kv_indices=kv,
         kv_indptr=indptr,
+        last_page_len=None if indptr is None else torch.empty(inputs.n_requests, dtype=i32, device=device),
         counts=torch.empty((inputs.n_requests, 3), dtype=i32, device=device),
         status=torch.zeros(1, dtype=i32, device=device),
         workspace=torch.empty(max(8, (ws_bytes + 7) // 8), dtype=torch.int64, device=device),
@@ -143,7 +145,7 @@ def allocate_outputs(inputs, device, *, generated_total=None):
 
 
 def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_pointers=None,
-                 generated=None, birth_slots=None):
+                 generated=None, birth_slots=None, page_size=1):
     """Rewrite each request's raw row to its terminal form and emit the lists.
 
     ``req_to_token``: int32 ``[pool_rows, width]`` request table (rows hold the
@@ -200,6 +202,8 @@ def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_po
             _lib.ptr(outputs.kv_indices),
             outputs.kv_indices.numel() if outputs.kv_indices is not None else 0,
             _lib.ptr(outputs.kv_indptr),
+            _lib.ptr(outputs.last_page_len),
+            int(page_size),
             outputs.counts.data_ptr(),
             outputs.workspace.data_ptr(),
             outputs.workspace.numel() * 8,

@@ -119,6 +119,102 @@ class Pipeline:
         torch.sum(self.flush_buf, 0, out=self.flush_out)
 
 
+def _time_steps(fn, steps, warmup, iters, flush):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    warm = a.elapsed_time(b) / steps
+    cold = []
+    for _ in range(iters):
+        flush()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        cold.append(a.elapsed_time(b))
+    return warm, cold
+
+
+def _graph_steps(fn, steps):
+    """Back-to-back replays of the step captured once in a HIP graph (no host
+    launch overhead between kernels); the step allocates nothing and records
+    no memset."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def tiny_config(device, flush):
+    """2 layers x 2 KV heads x 64, 4096 tokens: cache-resident, latency-bound."""
+    pipe = Pipeline("tiny", device)
+    warm, cold = _time_steps(pipe.step, 50, 10, 50, flush)
+    graph = _graph_steps(pipe.step, 50)
+    return {
+        "workload": pipe.w.name, "tokens": pipe.n, "moved": pipe.moved,
+        "step_ms_back_to_back": round(warm, 5), "step_ms_graph_replay": round(graph, 5),
+        "step_p50_ms": round(percentile(cold, 50), 5),
+        "step_p99_ms": round(percentile(cold, 99), 5), "kernel_launches_per_step": 3,
+    }
+
+
+def ragged_config(device, flush):
+    """64 requests of 2k-64k tokens: batched compaction + kv_indptr / kv_indices / last-page rebuild."""
+    w = synth.workload("ragged-64")
+    t0 = time.perf_counter()
+    layouts = synth.compile_layouts(w)
+    compile_ms = (time.perf_counter() - t0) * 1e3
+    slots = synth.assign_slots(w, layouts)
+    inputs = tables.pack_compaction_inputs(layouts, device)
+    table = torch.full((w.n_requests, max(w.lengths) + 8), -1, dtype=torch.int32, device=device)
+    birth = torch.from_numpy(np.concatenate(slots.birth_rows)).to(device)
+    fresh = torch.from_numpy(np.concatenate(slots.fresh)).to(device)
+    out = tables.allocate_outputs(inputs, device, generated_total=w.n_requests)
+    gen = torch.ones(w.n_requests, dtype=torch.int32, device=device)
+    rows = torch.arange(w.n_requests, dtype=torch.int64, device=device)
+
+    def step():
+        tables.compact_rows(inputs, table, rows, fresh, out, generated=gen, birth_slots=birth)
+
+    warm, cold = _time_steps(step, 50, 10, 50, flush)
+    graph = _graph_steps(step, 50)
+    total = sum(w.lengths)
+    # bytes: keep + positions + birth slot read, row write, lists written
+    meta = total * (1 + 8 + 4 + 4) + 4 * inputs.retired_total + 16 * inputs.moved_total \
+        + 8 * inputs.kept_total + 4 * (inputs.kept_total + w.n_requests) + 12 * w.n_requests
+    entries = w.n_requests * -(-max(w.lengths) // (256 * 16))
+    return {
+        "workload": w.name, "requests": w.n_requests, "tokens": total, "kept": inputs.kept_total,
+        "moved": inputs.moved_total, "step_ms_back_to_back": round(warm, 5),
+        "step_ms_graph_replay": round(graph, 5),
+        "step_p50_ms": round(percentile(cold, 50), 5), "step_p99_ms": round(percentile(cold, 99), 5),
+        "kernel_launches_per_step": 2 if entries <= 4096 else 3,
+        "metadata_bytes": meta, "host_event_compile_ms": round(compile_ms, 1),
+    }
+
+
 def read_pmc_traffic():
     """HBM bytes per Reposition launch from the committed rocprof PMC summary."""
     if not PMC_SUMMARY.exists():
@@ -320,6 +416,9 @@ def main():
             "bytes_per_launch": pipe.alg_bytes,
         },
     }
+    if not args.reposition_only:
+        print("# secondary configurations ...", file=sys.stderr, flush=True)
+        result["other_configs"] = [tiny_config(device, pipe.flush), ragged_config(device, pipe.flush)]
     if not args.no_cpu_baseline:
         print("# cpu baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(pipe, args.cpu_seconds)

@@ -91,6 +91,7 @@ int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t max_tokens);
  *   kv_indices (opt.)   compacted rows, then generated[b] raw-row entries
  *                       after the prompt, laid out by kv_indptr
  *   kv_indptr  (opt.)   [B+1] exclusive scan of kept + generated
+ *   last_page_len (opt.) [B] ((kept + generated - 1) % page_size) + 1, 0 if empty
  *   counts     (opt.)   [B,3] kept, moved, retired
  *   status     (opt.)   device int32, set to 1 if fresh_count or a
  *                       capacity does not match (outputs are then partial)
@@ -112,7 +113,8 @@ int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets,
                      int32_t* raw_indices, int32_t* active_positions,
                      int64_t kept_capacity, const int32_t* generated,
                      int32_t* kv_indices, int64_t kv_capacity,
-                     int32_t* kv_indptr, int32_t* counts, void* workspace,
+                     int32_t* kv_indptr, int32_t* last_page_len,
+                     int32_t page_size, int32_t* counts, void* workspace,
                      int64_t workspace_bytes, int32_t* status, void* stream);
 
 /*

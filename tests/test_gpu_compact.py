@@ -48,6 +48,7 @@ def _check(w, layouts, slots, out, rows_after, tails, gen):
     kept_off = moved_off = retired_off = kv_off = 0
     indptr = out.kv_indptr.cpu().numpy() if out.kv_indptr is not None else None
     counts = out.counts.cpu().numpy()
+    last_page = out.last_page_len.cpu().numpy() if out.last_page_len is not None else None
     for b, lay in enumerate(layouts):
         want = occ.closed_form(slots.birth_rows[b], lay.keep_mask.numpy(), lay.birth_positions.numpy(),
                                lay.positions.numpy(), slots.fresh[b])
@@ -63,6 +64,8 @@ def _check(w, layouts, slots, out, rows_after, tails, gen):
         np.testing.assert_array_equal(out.raw_indices.cpu().numpy()[kept_off : kept_off + kept], want["raw_indices"])
         np.testing.assert_array_equal(out.active_positions.cpu().numpy()[kept_off : kept_off + kept], want["active_positions"])
         assert counts[b].tolist() == [kept, moved, retired]
+        if last_page is not None:
+            assert last_page[b] == (1 if kept + gen[b] > 0 else 0)
         if out.kv_indices is not None:
             assert indptr[b] == kv_off
             seg = out.kv_indices.cpu().numpy()[kv_off : kv_off + kept + gen[b]]
