@@ -1,0 +1,311 @@
+// GQA decode attention with attention sinks over compacted page-one indices
+// (gfx950, MFMA).  The consumer of the Drop + Reposition metadata: one decode
+// step reads each request's keys through kv_indptr / kv_indices (full layers)
+// or the window-limited indices (sliding-window layers) and normalises with a
+// per-head sink logit:
+//   o_h = sum_j exp(s_hj) v_j / (sum_j exp(s_hj) + exp(sink_h)),
+//   s_hj = scale * q_h . k_j
+// which equals the reference's o * sigmoid(lse - sink)
+// (akv/system/sglang/srt/layers/attention/context_backend.py:254-272).
+//
+// Split-K: workgroup = one wave = (chunk of kChunk keys, KV head, request).
+// Per 16-key tile:  S^T[16 keys x 16 heads] = K[16 x D] . Q^T[D x 16] on
+// v_mfma_f32_16x16x16_bf16 (the group's q heads padded to 16 rows), online
+// softmax per head (column), then O^T[D x 16] += V^T[D x 16] . P^T[16 x 16]
+// where P^T is already in the B-operand layout of the second MFMA (no
+// shuffle) and V goes through LDS to be read transposed.  A combine kernel
+// merges the chunks and the sink.
+//
+// MFMA 16x16x16 bf16 lane layout (verified on gfx950): lane l supplies
+// A[l%16][4(l/16)+i] and B[4(l/16)+i][l%16] and holds D[4(l/16)+i][l%16].
+#include <cmath>
+
+#include "common.h"
+
+namespace akv {
+namespace {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) u32x4 global_u32x4;
+
+constexpr int kChunk = 256;  // keys per workgroup
+constexpr int kTile = 16;    // keys per MFMA tile
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnArgs {
+  const __bf16* q;
+  int64_t q_stride_b, q_stride_h;
+  const __bf16* k;
+  const __bf16* v;
+  int64_t k_stride_slot, k_stride_head, v_stride_slot, v_stride_head;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const float* sinks;
+  float scale_log2;  // scale * log2(e)
+  void* out;
+  int32_t out_f32;
+  int64_t out_stride_b, out_stride_h;
+  int32_t n_requests, q_heads, kv_heads, group, chunks;
+  float* partial;  // [B][Hkv][chunks][16][D + 2]  (o..., m, l)
+};
+
+__device__ __forceinline__ short bf16_bits(float x) {
+  return __builtin_bit_cast(short, static_cast<__bf16>(x));
+}
+
+template <int D>
+__global__ void __launch_bounds__(64) decode_attention_partial_kernel(const AttnArgs a) {
+  constexpr int kSteps = D / 16;    // MFMA k-steps over the head dim
+  constexpr int kPer = D / 4;       // dims per lane for the K operand
+  __shared__ __attribute__((aligned(16))) __bf16 vtile[kTile][D];
+
+  const int lane = threadIdx.x;
+  const int chunk = blockIdx.x;
+  const int g = blockIdx.y;
+  const int b = blockIdx.z;
+  const int64_t begin = a.kv_indptr[b];
+  const int64_t len = a.kv_indptr[b + 1] - begin;
+  const int64_t c0 = static_cast<int64_t>(chunk) * kChunk;
+  float* part = a.partial + ((static_cast<int64_t>(b) * a.kv_heads + g) * a.chunks + chunk) * 16 * (D + 2);
+  const int col = lane & 15;   // head within the group (B / D layout column)
+  const int quad = lane >> 4;  // 0..3
+  if (c0 >= len) {
+    // empty chunk: neutral partial (m = -inf, l = 0)
+    if (quad == 0) {
+      part[col * (D + 2) + D] = -INFINITY;
+      part[col * (D + 2) + D + 1] = 0.f;
+    }
+    return;
+  }
+  const int64_t c1 = c0 + kChunk < len ? c0 + kChunk : len;
+
+  // Q^T operand: lane supplies q[head col][dims quad*kPer + 4s + i]
+  s16x4 qop[kSteps];
+  {
+    const bool live = col < a.group;
+    const __bf16* qrow = a.q + static_cast<int64_t>(b) * a.q_stride_b +
+                         static_cast<int64_t>(g * a.group + (live ? col : 0)) * a.q_stride_h + quad * kPer;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qop[s][i] = live ? __builtin_bit_cast(short, qrow[4 * s + i]) : short(0);
+  }
+
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  for (int64_t t0 = c0; t0 < c1; t0 += kTile) {
+    // this lane's key for the K operand / slot lookup: key t0 + col
+    const int64_t j = t0 + col;
+    const bool valid = j < c1;
+    const int32_t slot = valid ? a.kv_indices[begin + j] : 0;
+    // ---- S^T = K . Q^T
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    {
+      const __bf16* krow = a.k + static_cast<int64_t>(slot) * a.k_stride_slot +
+                           static_cast<int64_t>(g) * a.k_stride_head + quad * kPer;
+      u32x4 kv[kPer / 8];
+#pragma unroll
+      for (int r = 0; r < kPer / 8; ++r)
+        kv[r] = valid ? *((const global_u32x4*)(krow + 8 * r)) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) {
+        // dims quad*kPer + 4*st .. +3 live in kv[st / 2], words (st % 2) * 2 .. +1
+        const u32x4 w = kv[st >> 1];
+        const uint32_t lo = (st & 1) ? w.z : w.x;
+        const uint32_t hi = (st & 1) ? w.w : w.y;
+        s16x4 kop;
+        kop[0] = static_cast<short>(lo & 0xffff);
+        kop[1] = static_cast<short>(lo >> 16);
+        kop[2] = static_cast<short>(hi & 0xffff);
+        kop[3] = static_cast<short>(hi >> 16);
+        s = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(kop, qop[st], s, 0, 0, 0);
+      }
+    }
+    // lane holds S^T[keys t0 + 4*quad + i][head col]
+    float p[4];
+    float tile_max = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = t0 + 4 * quad + i < c1;
+      p[i] = ok ? s[i] * a.scale_log2 : -INFINITY;
+      tile_max = fmaxf(tile_max, p[i]);
+    }
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+    const float m_new = fmaxf(m_run, tile_max);
+    const float corr = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
+    float row = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = m_new == -INFINITY ? 0.f : exp2f(p[i] - m_new);
+      row += p[i];
+    }
+    row += __shfl_xor(row, 16);
+    row += __shfl_xor(row, 32);
+    l_run = l_run * corr + row;
+    m_run = m_new;
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) acc[t] *= corr;
+
+    // ---- V tile -> LDS (16 keys x D), zero rows past the chunk
+    {
+      constexpr int kUnits = kTile * D / 8;  // 16-byte units in the tile
+#pragma unroll
+      for (int u = lane; u < kUnits; u += 64) {
+        const int key = u / (D / 8);
+        const int part8 = u - key * (D / 8);
+        const int32_t ks = __shfl(slot, key);
+        const bool kvalid = t0 + key < c1;
+        u32x4 val = {0u, 0u, 0u, 0u};
+        if (kvalid)
+          val = *((const global_u32x4*)(a.v + static_cast<int64_t>(ks) * a.v_stride_slot +
+                                        static_cast<int64_t>(g) * a.v_stride_head + part8 * 8));
+        *reinterpret_cast<u32x4*>(&vtile[key][part8 * 8]) = val;
+      }
+    }
+    __syncthreads();
+    // ---- O^T += V^T . P^T ; P^T is this lane's B operand as is
+    s16x4 pop;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pop[i] = bf16_bits(p[i]);
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      s16x4 vop;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vop[i] = __builtin_bit_cast(short, vtile[4 * quad + i][16 * t + col]);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vop, pop, acc[t], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  // lane holds O^T[dims 16t + 4*quad + i][head col]; every lane of a column
+  // carries that head's m and l
+  if (col < a.group) {
+    float* ph = part + col * (D + 2);
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ph[16 * t + 4 * quad + i] = acc[t][i];
+    if (quad == 0) {
+      ph[D] = m_run;
+      ph[D + 1] = l_run;
+    }
+  }
+}
+
+// One workgroup per (request, q head): merge chunk partials and the sink.
+template <int D>
+__global__ void __launch_bounds__(D) decode_attention_combine_kernel(const AttnArgs a) {
+  const int b = blockIdx.x;
+  const int h = blockIdx.y;
+  const int g = h / a.group;
+  const int hl = h - g * a.group;
+  const int d = threadIdx.x;
+  const int64_t len = a.kv_indptr[b + 1] - a.kv_indptr[b];
+  const int used = static_cast<int>((len + kChunk - 1) / kChunk);
+  const float* base = a.partial + (static_cast<int64_t>(b) * a.kv_heads + g) * a.chunks * 16 * (D + 2);
+  float m = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
+  for (int c = 0; c < used; ++c) m = fmaxf(m, base[(c * 16 + hl) * (D + 2) + D]);
+  float l = (a.sinks && m != -INFINITY) ? exp2f(a.sinks[h] * kLog2e - m) : 0.f;
+  float o = 0.f;
+  for (int c = 0; c < used; ++c) {
+    const float* pc = base + (c * 16 + hl) * (D + 2);
+    const float mc = pc[D];
+    if (mc == -INFINITY) continue;
+    const float w = exp2f(mc - m);
+    l += pc[D + 1] * w;
+    o += pc[d] * w;
+  }
+  const float r = l > 0.f ? o / l : 0.f;
+  const int64_t at = static_cast<int64_t>(b) * a.out_stride_b + static_cast<int64_t>(h) * a.out_stride_h + d;
+  if (a.out_f32)
+    static_cast<float*>(a.out)[at] = r;
+  else
+    static_cast<__bf16*>(a.out)[at] = static_cast<__bf16>(r);
+}
+
+int64_t chunks_for(int64_t max_len) { return max_len <= 0 ? 1 : (max_len + kChunk - 1) / kChunk; }
+
+}  // namespace
+}  // namespace akv
+
+extern "C" int64_t akv_decode_attention_workspace_bytes(int32_t n_requests, int32_t kv_heads,
+                                                         int32_t head_dim, int64_t max_len) {
+  using namespace akv;
+  if (n_requests < 0 || kv_heads <= 0 || head_dim <= 0 || max_len < 0) return -1;
+  return static_cast<int64_t>(n_requests) * kv_heads * chunks_for(max_len) * 16 * (head_dim + 2) * 4;
+}
+
+extern "C" int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_buffer,
+                                    const void* v_buffer, int64_t k_stride_slot, int64_t k_stride_head,
+                                    int64_t v_stride_slot, int64_t v_stride_head, int32_t n_requests,
+                                    int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                                    const int32_t* kv_indptr, const int32_t* kv_indices, const float* sinks,
+                                    float scale, void* out, int32_t out_dtype, int64_t out_stride_b,
+                                    int64_t out_stride_h, int64_t max_len, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
+  using namespace akv;
+  if (n_requests < 0 || max_len < 0) return fail(AKV_EINVAL, "akv_decode_attention: negative size");
+  if (n_requests == 0) return AKV_OK;
+  if (head_dim != 64 && head_dim != 128)
+    return fail(AKV_EINVAL, "akv_decode_attention: head_dim %d (supported: 64, 128)", head_dim);
+  if (kv_heads <= 0 || q_heads % kv_heads != 0 || q_heads / kv_heads > 16)
+    return fail(AKV_EINVAL, "akv_decode_attention: %d q heads over %d KV heads (group <= 16)", q_heads,
+                kv_heads);
+  if (out_dtype != AKV_BF16 && out_dtype != AKV_F32)
+    return fail(AKV_EINVAL, "akv_decode_attention: output must be bf16 or f32");
+  if (!q || !k_buffer || !v_buffer || !kv_indptr || !kv_indices || !out || !workspace)
+    return fail(AKV_EINVAL, "akv_decode_attention: null device pointer");
+  if ((k_stride_slot | k_stride_head | v_stride_slot | v_stride_head) % 8 != 0 ||
+      ((reinterpret_cast<uintptr_t>(k_buffer) | reinterpret_cast<uintptr_t>(v_buffer)) & 15) != 0)
+    return fail(AKV_EINVAL, "akv_decode_attention: K/V rows must be 16-byte aligned");
+  if (n_requests > 65535 || kv_heads > 65535)
+    return fail(AKV_EINVAL, "akv_decode_attention: batch too large");
+  const int64_t need = akv_decode_attention_workspace_bytes(n_requests, kv_heads, head_dim, max_len);
+  if (workspace_bytes < need)
+    return fail(AKV_EINVAL, "akv_decode_attention: workspace holds %lld bytes, needs %lld",
+                static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+  AttnArgs a{};
+  a.q = static_cast<const __bf16*>(q);
+  a.q_stride_b = q_stride_b;
+  a.q_stride_h = q_stride_h;
+  a.k = static_cast<const __bf16*>(k_buffer);
+  a.v = static_cast<const __bf16*>(v_buffer);
+  a.k_stride_slot = k_stride_slot;
+  a.k_stride_head = k_stride_head;
+  a.v_stride_slot = v_stride_slot;
+  a.v_stride_head = v_stride_head;
+  a.kv_indptr = kv_indptr;
+  a.kv_indices = kv_indices;
+  a.sinks = sinks;
+  a.scale_log2 = scale * kLog2e;
+  a.out = out;
+  a.out_f32 = out_dtype == AKV_F32;
+  a.out_stride_b = out_stride_b;
+  a.out_stride_h = out_stride_h;
+  a.n_requests = n_requests;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.group = q_heads / kv_heads;
+  a.chunks = static_cast<int32_t>(chunks_for(max_len));
+  a.partial = static_cast<float*>(workspace);
+  hipStream_t st = as_stream(stream);
+  const dim3 grid(static_cast<unsigned>(a.chunks), static_cast<unsigned>(kv_heads),
+                  static_cast<unsigned>(n_requests));
+  if (head_dim == 64) {
+    hipLaunchKernelGGL(decode_attention_partial_kernel<64>, grid, dim3(64), 0, st, a);
+    int rc = check_launch("akv_decode_attention (partial)");
+    if (rc) return rc;
+    hipLaunchKernelGGL(decode_attention_combine_kernel<64>, dim3(n_requests, q_heads), dim3(64), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(decode_attention_partial_kernel<128>, grid, dim3(64), 0, st, a);
+    int rc = check_launch("akv_decode_attention (partial)");
+    if (rc) return rc;
+    hipLaunchKernelGGL(decode_attention_combine_kernel<128>, dim3(n_requests, q_heads), dim3(128), 0, st, a);
+  }
+  return check_launch("akv_decode_attention (combine)");
+}

@@ -121,8 +121,22 @@ def ragged_batch_workload(name, model, n_requests, n_lo, n_hi, k_lo, k_hi, f_lo,
     return Workload(name, model, tuple(lengths), tuple(spans), seed, max(lengths), 2 * total + 1)
 
 
+def decode_batch_workload(name, model, n_requests, n, k, lo, hi, fraction, seed0):
+    """Requests of equal length, each with its own seeded drop spans (seed0 + b)."""
+    spans = []
+    for b in range(n_requests):
+        rng = np.random.default_rng(seed0 + b)
+        spans.append(place_spans(rng, n, sample_span_lengths(rng, n, k, lo, hi, fraction)))
+    return Workload(name, model, (n,) * n_requests, tuple(spans), seed0, n, 2 * n * n_requests + 64)
+
+
 def workload(name):
     """The named synthetic configurations."""
+    if name == "gpt-oss-decode-32x32k":
+        # 32 GPT-OSS requests of 32768 tokens, 12 spans of 500-2000 dropping
+        # ~40% each (seeds 5 + b): the decode consumer check
+        return decode_batch_workload("gpt-oss-120b-decode-32x32k", GPT_OSS_120B, 32, 32768, 12, 500, 2000,
+                                     0.40, seed0=5)
     if name == "tiny":
         # 2 layers x 2 KV heads x 64, plain RoPE; 4096 tokens, 3 spans of
         # 200-600 tokens dropping 25%

@@ -175,6 +175,38 @@ int akv_write_row_slots(const int64_t* pointers, const void* rows,
                         int32_t values_dtype, int64_t n, void* stream);
 
 /*
+ * Device bytes of the split-K scratch of akv_decode_attention.
+ */
+int64_t akv_decode_attention_workspace_bytes(int32_t n_requests,
+                                             int32_t kv_heads, int32_t head_dim,
+                                             int64_t max_len);
+
+/*
+ * One GQA decode step over compacted page-one indices with per-head sink
+ * logits: for request b and q head h (KV head h / (q_heads / kv_heads)),
+ *   out[b, h] = sum_j e^{s_j} v_j / (sum_j e^{s_j} + e^{sinks[h]}),
+ *   s_j = scale * q[b, h] . k_j, j over kv_indices[kv_indptr[b] ..
+ *   kv_indptr[b+1]) (no sink term when sinks == NULL).  bf16 q / K / V,
+ * head_dim 64 or 128, at most 16 q heads per KV head; max_len bounds every
+ * request's key count (it sizes the split).  out is bf16 or f32.
+ * The consumer of the compacted metadata (the reference's sink
+ * normalisation o * sigmoid(lse - sink),
+ * akv/system/sglang/srt/layers/attention/context_backend.py:254-272, over the
+ * decode indices of context_page_table.py:34-76).
+ */
+int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                         const void* k_buffer, const void* v_buffer,
+                         int64_t k_stride_slot, int64_t k_stride_head,
+                         int64_t v_stride_slot, int64_t v_stride_head,
+                         int32_t n_requests, int32_t q_heads, int32_t kv_heads,
+                         int32_t head_dim, const int32_t* kv_indptr,
+                         const int32_t* kv_indices, const float* sinks,
+                         float scale, void* out, int32_t out_dtype,
+                         int64_t out_stride_b, int64_t out_stride_h,
+                         int64_t max_len, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
+/*
  * Host event compiler (CPU, no device work).  Replays Drop and Reposition
  * events over the raw token stream.  Two calls, like the reference's count
  * and fill passes: akv_plan_count returns the number of transitions through
