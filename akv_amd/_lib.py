@@ -33,6 +33,11 @@ _SIGNATURES = {
         [c_int32, _P, c_int64, _P, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, c_int64,
          _P, _P, _P, _P, _P, c_int64, _P, _P, c_int64, _P, _P, c_int32, _P, _P, c_int64, _P, _P],
     ),
+    "akv_compact_pages": (
+        c_int32,
+        [c_int32, _P, c_int64, c_int32, _P, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+         _P, _P, _P, _P, _P, _P],
+    ),
     "akv_decode_indices": (
         c_int32,
         [_P, _P, c_int64, _P, c_int32, _P, c_int32, _P, c_int32, _P, c_int32, _P, c_int32,

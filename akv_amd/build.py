@@ -22,7 +22,9 @@ OUT_DIR = HERE / "_build"
 LIBRARY = HERE / "libakv_amd.so"
 ARCH = "gfx950"
 
-HIP_SOURCES = ["common.hip", "reposition.hip", "compact.hip", "decode_meta.hip", "decode_attention.hip"]
+HIP_SOURCES = [
+    "common.hip", "reposition.hip", "compact.hip", "compact_pages.hip", "decode_meta.hip", "decode_attention.hip",
+]
 CXX_SOURCES = ["event_plan.cpp"]
 
 COMMON_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-result"]

@@ -55,6 +55,9 @@ __device__ __forceinline__ short bf16_bits(float x) {
   return __builtin_bit_cast(short, static_cast<__bf16>(x));
 }
 
+// Workgroup = one wave = (chunk of kChunk keys, KV head, request).  (Putting
+// all KV heads of a chunk in one workgroup, so key rows are read whole,
+// measured slower: the per-tile barrier then couples 8 waves.)
 template <int D>
 __global__ void __launch_bounds__(64) decode_attention_partial_kernel(const AttnArgs a) {
   constexpr int kSteps = D / 16;    // MFMA k-steps over the head dim
@@ -98,33 +101,55 @@ __global__ void __launch_bounds__(64) decode_attention_partial_kernel(const Attn
   for (int t = 0; t < D / 16; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  for (int64_t t0 = c0; t0 < c1; t0 += kTile) {
+  // Registers of one 16-key tile between its global loads and its use.
+  constexpr int kVUnits = kTile * D / 8 / 64;  // 16-byte V units per lane
+  struct Tile {
+    u32x4 k[kPer / 8];
+    u32x4 v[kVUnits];
+  };
+  auto load_tile = [&](int64_t t0) {
+    Tile r;
     // this lane's key for the K operand / slot lookup: key t0 + col
-    const int64_t j = t0 + col;
-    const bool valid = j < c1;
-    const int32_t slot = valid ? a.kv_indices[begin + j] : 0;
+    const bool valid = t0 + col < c1;
+    const int32_t slot = valid ? a.kv_indices[begin + t0 + col] : 0;
+    const __bf16* krow =
+        a.k + static_cast<int64_t>(slot) * a.k_stride_slot + static_cast<int64_t>(g) * a.k_stride_head + quad * kPer;
+#pragma unroll
+    for (int q8 = 0; q8 < kPer / 8; ++q8)
+      r.k[q8] = valid ? *((const global_u32x4*)(krow + 8 * q8)) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q8 = 0; q8 < kVUnits; ++q8) {
+      const int u = lane + 64 * q8;
+      const int key = u / (D / 8);
+      const int part8 = u - key * (D / 8);
+      const int32_t ks = __shfl(slot, key);
+      r.v[q8] = t0 + key < c1 ? *((const global_u32x4*)(a.v + static_cast<int64_t>(ks) * a.v_stride_slot +
+                                                        static_cast<int64_t>(g) * a.v_stride_head + part8 * 8))
+                              : u32x4{0u, 0u, 0u, 0u};
+    }
+    return r;
+  };
+
+  // Software-pipelined: the next tile's K and V loads are in flight while
+  // this tile's MFMAs and softmax run.
+  Tile cur = load_tile(c0);
+  for (int64_t t0 = c0; t0 < c1; t0 += kTile) {
+    Tile nxt = cur;
+    if (t0 + kTile < c1) nxt = load_tile(t0 + kTile);
     // ---- S^T = K . Q^T
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    {
-      const __bf16* krow = a.k + static_cast<int64_t>(slot) * a.k_stride_slot +
-                           static_cast<int64_t>(g) * a.k_stride_head + quad * kPer;
-      u32x4 kv[kPer / 8];
 #pragma unroll
-      for (int r = 0; r < kPer / 8; ++r)
-        kv[r] = valid ? *((const global_u32x4*)(krow + 8 * r)) : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int st = 0; st < kSteps; ++st) {
-        // dims quad*kPer + 4*st .. +3 live in kv[st / 2], words (st % 2) * 2 .. +1
-        const u32x4 w = kv[st >> 1];
-        const uint32_t lo = (st & 1) ? w.z : w.x;
-        const uint32_t hi = (st & 1) ? w.w : w.y;
-        s16x4 kop;
-        kop[0] = static_cast<short>(lo & 0xffff);
-        kop[1] = static_cast<short>(lo >> 16);
-        kop[2] = static_cast<short>(hi & 0xffff);
-        kop[3] = static_cast<short>(hi >> 16);
-        s = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(kop, qop[st], s, 0, 0, 0);
-      }
+    for (int st = 0; st < kSteps; ++st) {
+      // dims quad*kPer + 4*st .. +3 live in k[st / 2], words (st % 2) * 2 .. +1
+      const u32x4 w = cur.k[st >> 1];
+      const uint32_t lo = (st & 1) ? w.z : w.x;
+      const uint32_t hi = (st & 1) ? w.w : w.y;
+      s16x4 kop;
+      kop[0] = static_cast<short>(lo & 0xffff);
+      kop[1] = static_cast<short>(lo >> 16);
+      kop[2] = static_cast<short>(hi & 0xffff);
+      kop[3] = static_cast<short>(hi >> 16);
+      s = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(kop, qop[st], s, 0, 0, 0);
     }
     // lane holds S^T[keys t0 + 4*quad + i][head col]
     float p[4];
@@ -152,21 +177,12 @@ __global__ void __launch_bounds__(64) decode_attention_partial_kernel(const Attn
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) acc[t] *= corr;
 
-    // ---- V tile -> LDS (16 keys x D), zero rows past the chunk
-    {
-      constexpr int kUnits = kTile * D / 8;  // 16-byte units in the tile
+    // ---- V tile -> LDS (16 keys x D); rows past the chunk were loaded as 0
 #pragma unroll
-      for (int u = lane; u < kUnits; u += 64) {
-        const int key = u / (D / 8);
-        const int part8 = u - key * (D / 8);
-        const int32_t ks = __shfl(slot, key);
-        const bool kvalid = t0 + key < c1;
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (kvalid)
-          val = *((const global_u32x4*)(a.v + static_cast<int64_t>(ks) * a.v_stride_slot +
-                                        static_cast<int64_t>(g) * a.v_stride_head + part8 * 8));
-        *reinterpret_cast<u32x4*>(&vtile[key][part8 * 8]) = val;
-      }
+    for (int q8 = 0; q8 < kVUnits; ++q8) {
+      const int u = lane + 64 * q8;
+      const int key = u / (D / 8);
+      *reinterpret_cast<u32x4*>(&vtile[key][(u - key * (D / 8)) * 8]) = cur.v[q8];
     }
     __syncthreads();
     // ---- O^T += V^T . P^T ; P^T is this lane's B operand as is
@@ -181,6 +197,7 @@ __global__ void __launch_bounds__(64) decode_attention_partial_kernel(const Attn
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vop, pop, acc[t], 0, 0, 0);
     }
     __syncthreads();
+    cur = nxt;
   }
   // lane holds O^T[dims 16t + 4*quad + i][head col]; every lane of a column
   // carries that head's m and l
@@ -296,13 +313,14 @@ extern "C" int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q
   hipStream_t st = as_stream(stream);
   const dim3 grid(static_cast<unsigned>(a.chunks), static_cast<unsigned>(kv_heads),
                   static_cast<unsigned>(n_requests));
+  const dim3 block(64);
   if (head_dim == 64) {
-    hipLaunchKernelGGL(decode_attention_partial_kernel<64>, grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL(decode_attention_partial_kernel<64>, grid, block, 0, st, a);
     int rc = check_launch("akv_decode_attention (partial)");
     if (rc) return rc;
     hipLaunchKernelGGL(decode_attention_combine_kernel<64>, dim3(n_requests, q_heads), dim3(64), 0, st, a);
   } else {
-    hipLaunchKernelGGL(decode_attention_partial_kernel<128>, grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL(decode_attention_partial_kernel<128>, grid, block, 0, st, a);
     int rc = check_launch("akv_decode_attention (partial)");
     if (rc) return rc;
     hipLaunchKernelGGL(decode_attention_combine_kernel<128>, dim3(n_requests, q_heads), dim3(128), 0, st, a);

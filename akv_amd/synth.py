@@ -13,7 +13,7 @@ counts as unmapped); the request's birth slots are a seeded permutation of
 the free slots and its fresh slots the next ones in that permutation.
 """
 
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import numpy as np
 import torch
@@ -48,6 +48,8 @@ LLAMA3_8B = Model(
          high_freq_factor=4.0),
 )
 
+LLAMA3_8B_2L = replace(LLAMA3_8B, name="llama-3-8b shape with 2 layers", n_layers=2)
+
 
 @dataclass(frozen=True)
 class Workload:
@@ -58,6 +60,8 @@ class Workload:
     seed: int
     table_positions: int
     pool_slots: int
+    page_size: int = 1
+    shared_prefix: int = 0  # raw tokens [0, shared_prefix) of every request share pages
 
     @property
     def n_requests(self):
@@ -130,6 +134,105 @@ def decode_batch_workload(name, model, n_requests, n, k, lo, hi, fraction, seed0
     return Workload(name, model, (n,) * n_requests, tuple(spans), seed0, n, 2 * n * n_requests + 64)
 
 
+def shared_prefix_workload(name, model, n_requests, prefix, suffix_lo, suffix_hi, k_lo, k_hi, span_lo,
+                           span_hi, page_size, seed):
+    """Requests sharing a page-aligned prefix, each with a private suffix and
+    ``k ~ U{k_lo..k_hi}`` dropped spans of ``U[span_lo, span_hi]`` tokens
+    placed inside the prefix."""
+    if prefix % page_size:
+        raise ValueError("the shared prefix must be page aligned")
+    rng = np.random.default_rng(seed)
+    lengths, spans = [], []
+    for _ in range(n_requests):
+        suffix = int(rng.integers(suffix_lo, suffix_hi + 1))
+        k = int(rng.integers(k_lo, k_hi + 1))
+        spans.append(place_spans(rng, prefix, rng.integers(span_lo, span_hi + 1, size=k)))
+        lengths.append(prefix + suffix)
+    return Workload(name, model, tuple(lengths), tuple(spans), seed, max(lengths), 0, page_size, prefix)
+
+
+def paged_demand(w):
+    """Per request: (kept, first copied page, fresh pages) of a shared-prefix workload."""
+    P = w.page_size
+    out = []
+    for n, spans in zip(w.lengths, w.spans):
+        dropped = sum(e - s for s, e in spans)
+        kept = n - dropped
+        p0 = spans[0][0] // P if spans else -(-n // P)
+        out.append((kept, p0, max(0, -(-kept // P) - p0)))
+    return out
+
+
+@dataclass
+class PageAssignment:
+    shared_pages: np.ndarray  # int32 [prefix / P]
+    birth_rows: list  # per request: int32 token slots in raw order
+    fresh_pages: list  # per request: int32 pages for its copied logical pages
+    pool_pages: int
+    groups: tuple  # requests processed together, in order
+
+
+def assign_pages(w, groups=None):
+    """Physical pages of a shared-prefix workload (page 0 is reserved padding).
+
+    Requests run in ``groups`` (default: all at once).  A group's fresh pages
+    come first from pages freed by earlier groups -- their private suffix
+    pages, and shared pages whose last reference they dropped -- then from
+    spare pages, so peak memory is the old pages plus the largest shortfall
+    rather than old plus all fresh pages.  Page ids are a seeded permutation.
+    """
+    P = w.page_size
+    B = w.n_requests
+    groups = tuple(tuple(g) for g in (groups or [range(B)]))
+    if sorted(b for g in groups for b in g) != list(range(B)):
+        raise ValueError("groups must cover every request once")
+    shared_n = w.shared_prefix // P
+    suffix_n = [-(-(n - w.shared_prefix) // P) for n in w.lengths]
+    demand = paged_demand(w)
+
+    def simulate(shared, private, spare):
+        free, spare_at, fresh = [], 0, [None] * B
+        refs = np.full(shared_n, B, dtype=np.int64)
+        for g in groups:
+            need = sum(demand[b][2] for b in g)
+            take = free[:need]
+            free = free[need:]
+            extra = need - len(take)
+            if spare is not None:
+                take = take + list(spare[spare_at : spare_at + extra])
+            spare_at += extra
+            at = 0
+            for b in g:
+                fresh[b] = np.asarray(take[at : at + demand[b][2]], dtype=np.int32)
+                at += demand[b][2]
+            for b in g:
+                p0 = demand[b][1]
+                free.extend(private[b][max(0, p0 - shared_n):])
+                refs[min(p0, shared_n):] -= 1
+            for p in np.flatnonzero(refs == 0):
+                free.append(shared[p])
+                refs[p] = -1
+        return fresh, spare_at
+
+    _, spare_n = simulate(np.zeros(shared_n, np.int32), [[0] * s for s in suffix_n], None)
+    pool_pages = 1 + shared_n + sum(suffix_n) + spare_n
+    rng = np.random.default_rng(w.seed + 1000)
+    perm = rng.permutation(np.arange(1, pool_pages, dtype=np.int64)).astype(np.int32)
+    shared = perm[:shared_n]
+    at = shared_n
+    private = []
+    for s in suffix_n:
+        private.append(list(perm[at : at + s]))
+        at += s
+    fresh, _ = simulate(shared, private, perm[at:])
+    rows = []
+    for n, priv in zip(w.lengths, private):
+        pages = np.concatenate((shared, np.asarray(priv, dtype=np.int32)))
+        i = np.arange(n)
+        rows.append((pages[i // P].astype(np.int64) * P + i % P).astype(np.int32))
+    return PageAssignment(shared, rows, fresh, pool_pages, groups)
+
+
 def workload(name):
     """The named synthetic configurations."""
     if name == "gpt-oss-decode-32x32k":
@@ -146,6 +249,16 @@ def workload(name):
         # tokens dropping ~40%
         return single_request_workload("gpt-oss-120b-32k", GPT_OSS_120B, 32768, 12, 500, 2000, 0.40,
                                        seed=2)
+    if name == "llama3-cow-16":
+        # Llama-3-8B shape, page 16: 16 requests share an 8192-token prefix
+        # (512 pages), each adds a private 16384-122880-token suffix and drops
+        # 1-3 spans of 64-512 tokens inside the prefix (copy-on-write)
+        return shared_prefix_workload("llama3-8b-cow-16x(8k+[16k,120k])", LLAMA3_8B, 16, 8192, 16384, 122880,
+                                      1, 3, 64, 512, 16, seed=4)
+    if name == "llama3-cow-small":
+        # the same events with 2 layers and 256-1024-token suffixes
+        return shared_prefix_workload("llama3-8b-2l-cow-16x(8k+[256,1024])", LLAMA3_8B_2L, 16, 8192, 256,
+                                      1024, 1, 3, 64, 512, 16, seed=4)
     if name == "ragged-64":
         # 64 requests of 2048-65536 tokens, 1-8 spans dropping 10-60% each
         return ragged_batch_workload("ragged-64x[2k,64k]", GPT_OSS_120B, 64, 2048, 65536, 1, 8, 0.10,

@@ -173,6 +173,8 @@ def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_po
         raise ValueError("birth_slots must be int32 with one slot per raw token")
     if generated is not None and outputs.kv_indices is None:
         raise ValueError("generated entries need kv_indices outputs")
+    if row_pointers is None and req_to_token.shape[1] < inputs.max_tokens:
+        raise ValueError("req_to_token rows are shorter than the longest request")
     lib = _lib.load()
     device = req_to_token.device
     with _on_device(device):
@@ -211,4 +213,173 @@ def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_po
             current_stream_handle(device),
         )
     _lib.check(rc, "akv_compact_rows")
+    return outputs
+
+
+# ---------------------------------------------------------------------------
+# Page-granular compaction with copy-on-write (page_size > 1).
+
+
+@dataclass
+class PagedInputs:
+    """Device metadata of a paged batch plus the per-request counts (host)."""
+
+    req_offsets: torch.Tensor  # int64 [B+1]
+    keep: torch.Tensor  # uint8 [N]
+    birth_positions: torch.Tensor  # int32 [N]
+    final_positions: torch.Tensor  # int32 [N]
+    bases: torch.Tensor  # int64 [6, B+1]
+    page_size: int
+    n_tokens: tuple
+    kept: tuple
+    first_copied_page: tuple
+    copies: tuple
+    fresh_pages: tuple
+    new_pages: tuple
+    released_pages: tuple
+
+    @property
+    def n_requests(self):
+        return len(self.n_tokens)
+
+    @property
+    def max_tokens(self):
+        return max(self.n_tokens) if self.n_tokens else 0
+
+
+def _paged_counts(keep, final, page_size):
+    n = len(keep)
+    kept = int(keep.sum())
+    if not np.array_equal(final[keep], np.arange(kept)):
+        raise ValueError("paged compaction needs compact final positions (a closing Reposition)")
+    dropped = np.flatnonzero(~keep)
+    p0 = int(dropped[0]) // page_size if len(dropped) else -(-n // page_size)
+    copy_from = p0 * page_size
+    copies = max(0, kept - copy_from)
+    new_pages = -(-kept // page_size)
+    fresh = max(0, new_pages - p0)
+    released = max(0, -(-n // page_size) - p0)
+    return kept, p0, copy_from, copies, fresh, new_pages, released
+
+
+def pack_paged_inputs(layouts, page_size, device):
+    """One host-to-device copy of keep / birth / final plus the per-request bases.
+
+    Request ``b`` keeps logical pages ``< p0_b`` (``p0`` = page of its first
+    dropped token) and moves every kept token of rank ``>= p0_b * P`` into
+    fresh pages; all offsets follow from the CPU layout.
+    """
+    if page_size < 1:
+        raise ValueError("page_size must be positive")
+    keeps, births, finals, stats = [], [], [], []
+    for layout in layouts:
+        keep = np.asarray(layout.keep_mask, dtype=bool)
+        final = np.asarray(layout.positions, dtype=np.int32)
+        keeps.append(keep)
+        births.append(np.asarray(layout.birth_positions, dtype=np.int32))
+        finals.append(final)
+        stats.append((len(keep),) + _paged_counts(keep, final, page_size))
+    B = len(stats)
+    ns = [s[0] for s in stats]
+    bases = np.zeros((6, B + 1), dtype=np.int64)
+    bases[0, :B] = [s[3] for s in stats]  # copy_from
+    for row, col in ((1, 1), (2, 4), (3, 5), (4, 6), (5, 7)):
+        bases[row, 1:] = np.cumsum([s[col] for s in stats])
+    total = sum(ns)
+    offsets = np.zeros(B + 1, dtype=np.int64)
+    offsets[1:] = np.cumsum(ns)
+    keep_words = (total + 3) // 4
+    words = 2 * total + 2 * (B + 1) + 2 * bases.size + keep_words
+    packed = np.zeros(words, dtype=np.int32)
+    at = 0
+    for arr in (np.concatenate(births) if total else np.zeros(0, np.int32),
+                np.concatenate(finals) if total else np.zeros(0, np.int32)):
+        packed[at : at + total] = arr
+        at += total
+    packed[at : at + 2 * (B + 1)] = offsets.view(np.int32)
+    at_off = at
+    at += 2 * (B + 1)
+    packed[at : at + 2 * bases.size] = bases.reshape(-1).view(np.int32)
+    at_bases = at
+    at += 2 * bases.size
+    if total:
+        packed[at:].view(np.uint8)[:total] = np.concatenate(keeps).astype(np.uint8)
+    host = torch.from_numpy(packed)
+    if torch.cuda.is_available():
+        host = host.pin_memory()
+    dev = host.to(device, non_blocking=True)
+    return PagedInputs(
+        req_offsets=dev[at_off : at_off + 2 * (B + 1)].view(torch.int64),
+        keep=dev[at:].view(torch.uint8)[:total],
+        birth_positions=dev[:total],
+        final_positions=dev[total : 2 * total],
+        bases=dev[at_bases : at_bases + 2 * bases.size].view(torch.int64).view(6, B + 1),
+        page_size=page_size,
+        n_tokens=tuple(ns),
+        kept=tuple(s[1] for s in stats),
+        first_copied_page=tuple(s[2] for s in stats),
+        copies=tuple(s[4] for s in stats),
+        fresh_pages=tuple(s[5] for s in stats),
+        new_pages=tuple(s[6] for s in stats),
+        released_pages=tuple(s[7] for s in stats),
+    )
+
+
+@dataclass
+class PagedOutputs:
+    copy_src: torch.Tensor
+    copy_dst: torch.Tensor
+    copy_pairs: torch.Tensor
+    released_pages: torch.Tensor
+    page_table: torch.Tensor
+    raw_indices: torch.Tensor
+    active_positions: torch.Tensor
+
+
+def allocate_paged_outputs(inputs, device):
+    i32 = torch.int32
+    copies = sum(inputs.copies)
+    kept = sum(inputs.kept)
+    return PagedOutputs(
+        copy_src=torch.empty(copies, dtype=i32, device=device),
+        copy_dst=torch.empty(copies, dtype=i32, device=device),
+        copy_pairs=torch.empty((copies, 2), dtype=i32, device=device),
+        released_pages=torch.empty(sum(inputs.released_pages), dtype=i32, device=device),
+        page_table=torch.empty(sum(inputs.new_pages), dtype=i32, device=device),
+        raw_indices=torch.empty(kept, dtype=i32, device=device),
+        active_positions=torch.empty(kept, dtype=i32, device=device),
+    )
+
+
+def compact_pages(inputs, req_to_token, req_rows, fresh_pages, outputs, *, row_pointers=None, birth_slots=None):
+    """Rewrite each request's raw row page-dense; emit copies, released pages and page tables.
+
+    ``fresh_pages``: int32 page ids, request-major, ``inputs.fresh_pages[b]``
+    per request (the allocator's pages for the copied logical pages).
+    """
+    if req_to_token.dtype != torch.int32 or req_to_token.ndim != 2 or req_to_token.stride(1) != 1:
+        raise ValueError("req_to_token must be an int32 [rows, width] table with unit column stride")
+    if req_rows.dtype != torch.int64 or req_rows.shape != (inputs.n_requests,):
+        raise ValueError("req_rows must be int64 [B]")
+    if fresh_pages.dtype != torch.int32 or fresh_pages.shape != (sum(inputs.fresh_pages),):
+        raise ValueError("fresh_pages must be int32 with one page per copied logical page")
+    if birth_slots is not None and (birth_slots.dtype != torch.int32 or birth_slots.shape != (sum(inputs.n_tokens),)):
+        raise ValueError("birth_slots must be int32 with one slot per raw token")
+    if row_pointers is not None and row_pointers.dtype != torch.int64:
+        raise ValueError("row_pointers must be int64 addresses")
+    if row_pointers is None and req_to_token.shape[1] < inputs.max_tokens:
+        raise ValueError("req_to_token rows are shorter than the longest request")
+    lib = _lib.load()
+    device = req_to_token.device
+    with _on_device(device):
+        rc = lib.akv_compact_pages(
+            inputs.n_requests, inputs.req_offsets.data_ptr(), inputs.max_tokens, inputs.page_size,
+            req_to_token.data_ptr(), req_to_token.stride(0), _lib.ptr(row_pointers), req_rows.data_ptr(),
+            inputs.keep.data_ptr(), inputs.birth_positions.data_ptr(), inputs.final_positions.data_ptr(),
+            _lib.ptr(birth_slots), inputs.bases.data_ptr(), _lib.ptr(fresh_pages) if fresh_pages.numel() else None,
+            outputs.copy_src.data_ptr(), outputs.copy_dst.data_ptr(), outputs.copy_pairs.data_ptr(),
+            outputs.released_pages.data_ptr(), outputs.page_table.data_ptr(), outputs.raw_indices.data_ptr(),
+            outputs.active_positions.data_ptr(), current_stream_handle(device),
+        )
+    _lib.check(rc, "akv_compact_pages")
     return outputs

@@ -215,6 +215,72 @@ def ragged_config(device, flush):
     }
 
 
+def decode_consumer_config(device, flush):
+    """GPT-OSS decode step (32 requests x 32k, 64 q / 8 KV heads, sinks) over the
+    compacted metadata: full layer and 128-token sliding-window layer."""
+    import dataclasses
+
+    from akv_amd import attention, page_table
+
+    w = synth.workload("gpt-oss-decode-32x32k")
+    model = dataclasses.replace(w.model, n_layers=2)
+    layouts = synth.compile_layouts(w)
+    slots = synth.assign_slots(w, layouts)
+    B, n = w.n_requests, w.lengths[0]
+    used = np.concatenate(slots.birth_rows + slots.fresh)
+    gen_slot = np.setdiff1d(np.arange(1, w.pool_slots), used)[:B].astype(np.int32)
+    table = torch.full((B, n + 4), -1, dtype=torch.int32)
+    table[:, n] = torch.from_numpy(gen_slot)
+    table = table.to(device)
+    inputs = tables.pack_compaction_inputs(layouts, device)
+    out = tables.allocate_outputs(inputs, device, generated_total=B)
+    rows = torch.arange(B, dtype=torch.int64, device=device)
+    tables.compact_rows(inputs, table, rows, torch.from_numpy(np.concatenate(slots.fresh)).to(device), out,
+                        generated=torch.ones(B, dtype=torch.int32, device=device),
+                        birth_slots=torch.from_numpy(np.concatenate(slots.birth_rows)).to(device))
+    pool = synth.make_pool(model, w.pool_slots, device, seed=9, generate_on_device=True)
+
+    class _T:
+        page_size, defer_read_translate, is_translating = 1, False, False
+        req_to_token = table
+
+    registry = page_table.ContextDecodeRegistry(_T(), pool=None)
+    kept_off = np.concatenate(([0], np.cumsum(inputs.kept)))
+    registry.rows[rows] = torch.tensor(
+        [(out.raw_indices.data_ptr() + 4 * int(kept_off[b]), out.active_positions.data_ptr() + 4 * int(kept_off[b]),
+          n, inputs.kept[b], layouts[b].next_position, 0) for b in range(B)], dtype=torch.int64).to(device)
+    seq = torch.tensor([k + 1 for k in inputs.kept], dtype=torch.int64, device=device)
+    win_indptr = torch.zeros(B + 1, dtype=torch.int32, device=device)
+    win_idx = torch.zeros(B * 129, dtype=torch.int32, device=device)
+    registry.fill_window(rows, seq, win_indptr, 128, win_idx)
+    q = torch.randn((B, 64, 64), device=device).to(torch.bfloat16)
+    sinks = torch.randn(64, device=device)
+    o = torch.empty((B, 64, 64), dtype=torch.bfloat16, device=device)
+    max_full = max(inputs.kept) + 1
+    ws = torch.empty(attention.workspace_bytes(B, 8, 64, max_full) // 4 + 1, dtype=torch.float32, device=device)
+
+    def full():
+        attention.decode_attention(q, pool.k[1], pool.v[1], out.kv_indptr, out.kv_indices, o, scale=0.125,
+                                   max_len=max_full, sinks=sinks, workspace=ws)
+
+    def windowed():
+        attention.decode_attention(q, pool.k[0], pool.v[0], win_indptr, win_idx, o, scale=0.125, max_len=129,
+                                   sinks=sinks, workspace=ws)
+
+    warm_full, cold_full = _time_steps(full, 20, 5, 20, flush)
+    warm_win, cold_win = _time_steps(windowed, 50, 5, 20, flush)
+    keys = inputs.kept_total + B
+    kv_bytes = keys * 8 * 64 * 2 * 2  # K and V rows of 8 KV heads
+    return {
+        "workload": w.name + " decode step (64 q / 8 KV heads, sinks)",
+        "keys_full_layer": keys,
+        "full_layer_ms": round(warm_full, 5), "full_layer_p50_ms": round(percentile(cold_full, 50), 5),
+        "full_layer_kv_GBs": round(kv_bytes / (warm_full / 1e3) / 1e9, 1),
+        "window128_layer_ms": round(warm_win, 5), "window128_layer_p50_ms": round(percentile(cold_win, 50), 5),
+        "kernel_launches_per_layer": 2,
+    }
+
+
 def read_pmc_traffic():
     """HBM bytes per Reposition launch from the committed rocprof PMC summary."""
     if not PMC_SUMMARY.exists():
@@ -418,7 +484,8 @@ def main():
     }
     if not args.reposition_only:
         print("# secondary configurations ...", file=sys.stderr, flush=True)
-        result["other_configs"] = [tiny_config(device, pipe.flush), ragged_config(device, pipe.flush)]
+        result["other_configs"] = [tiny_config(device, pipe.flush), ragged_config(device, pipe.flush),
+                                   decode_consumer_config(device, pipe.flush)]
     if not args.no_cpu_baseline:
         print("# cpu baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(pipe, args.cpu_seconds)

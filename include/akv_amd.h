@@ -118,6 +118,38 @@ int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets,
                      int64_t workspace_bytes, int32_t* status, void* stream);
 
 /*
+ * Page-granular compaction with copy-on-write, page_size P >= 1, for
+ * requests whose final positions are 0 .. kept-1 (a closing Reposition).
+ * Per request b (raw tokens req_offsets[b] .. req_offsets[b+1]):
+ *   p0 = first dropped raw token / P (ceil(n / P) when nothing is dropped);
+ *   logical pages < p0 keep their physical pages; every kept token of rank
+ *   r >= p0 * P moves to fresh_pages[fresh_b + r / P - p0] * P + r % P with
+ *   copy (old slot, new slot, (birth pos, r)); dropped tokens get -1;
+ *   released_pages lists old pages of logical index >= p0 (raw order);
+ *   page_table lists the new pages of the request, ceil(kept / P) of them.
+ * bases int64 [6, B+1], host-computed from the layout:
+ *   row 0: p0 * P per request; rows 1..5: exclusive offsets of kept
+ *   tokens, copies, fresh pages, page-table entries and released pages.
+ * One launch, one thread per raw token; every write is bounded by bases.
+ * No counterpart in the reference, whose Reposition rejects page_size != 1
+ * (akv/system/sglang/kernels/ops/attention/context_reposition.py:153-154);
+ * its P = 1 case equals akv_compact_rows' row/copy outputs
+ * (occurrence.py:632-767).
+ */
+int akv_compact_pages(int32_t n_requests, const int64_t* req_offsets,
+                      int64_t max_tokens, int32_t page_size, int32_t* table,
+                      int64_t row_stride, const int64_t* row_pointers,
+                      const int64_t* req_rows, const uint8_t* keep,
+                      const int32_t* birth_positions,
+                      const int32_t* final_positions,
+                      const int32_t* birth_slots, const int64_t* bases,
+                      const int32_t* fresh_pages, int32_t* copy_src,
+                      int32_t* copy_dst, int32_t* copy_pairs,
+                      int32_t* released_pages, int32_t* page_table,
+                      int32_t* raw_indices, int32_t* active_positions,
+                      void* stream);
+
+/*
  * Decode read indices over raw request rows through the registry rows
  * int64 [rows, 6] = (raw_ids_ptr, positions_ptr, prompt_len, active,
  * next_pos, row_ptr):

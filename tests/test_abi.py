@@ -49,6 +49,12 @@ def test_validation_rejects_before_any_device_work(lib):
     assert lib.akv_compact_rows(*zeros(lib.akv_compact_rows, a0=-1)) == _lib.AKV_EINVAL
     assert lib.akv_compact_rows(*zeros(lib.akv_compact_rows, a0=2)) == _lib.AKV_EINVAL
     assert "null device pointer" in _lib.last_error()
+    assert lib.akv_compact_pages(*zeros(lib.akv_compact_pages, a0=-1)) == _lib.AKV_EINVAL
+    assert lib.akv_compact_pages(*zeros(lib.akv_compact_pages)) == 0  # empty batch
+    assert lib.akv_compact_pages(*zeros(lib.akv_compact_pages, a0=2, a2=5)) == _lib.AKV_EINVAL
+    assert "page_size" in _lib.last_error()
+    assert lib.akv_compact_pages(*zeros(lib.akv_compact_pages, a0=2, a2=5, a3=16)) == _lib.AKV_EINVAL
+    assert "null device pointer" in _lib.last_error()
     ws = lib.akv_compact_workspace_bytes(64, 65536)
     assert ws > 0
     assert lib.akv_decode_indices(*zeros(lib.akv_decode_indices)) == 0

@@ -1,0 +1,197 @@
+"""GPU parity of page-granular compaction with copy-on-write (page size 16).
+
+Tables, copy lists, released pages and page tables bit-exact against the
+paging oracle; K re-rotated bit-exact and V moved bit for bit into fresh
+pages; shared prefix pages and every other slot left untouched.  With page
+size 1 the paged kernel reproduces ``akv_compact_rows``.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from akv_amd import ops, synth, tables
+from oracle import paging as pg
+from oracle import reposition as rp
+
+from helpers import storage_equal, to_storage
+
+pytestmark = pytest.mark.gpu
+
+
+def _table_for(rows, width, device, order):
+    table = torch.full((len(rows) + 3, width), -7, dtype=torch.int32)
+    for b, r in enumerate(rows):
+        table[order[b], : len(r)] = torch.from_numpy(r)
+    return table.to(device)
+
+
+def _run_groups(w, a, layouts, table, req_rows, device, pool=None, cos_sin=None, row_pointers=None):
+    """Compact (and reposition) group by group; return per-request device outputs."""
+    P = w.page_size
+    got = {}
+    for g in a.groups:
+        g = list(g)
+        inp = tables.pack_paged_inputs([layouts[b] for b in g], P, device)
+        out = tables.allocate_paged_outputs(inp, device)
+        fresh = np.concatenate([a.fresh_pages[b] for b in g]).astype(np.int32)
+        rows = torch.tensor([req_rows[b] for b in g], dtype=torch.int64, device=device)
+        tables.compact_pages(inp, table, rows, torch.from_numpy(fresh).to(device), out,
+                             row_pointers=row_pointers)
+        if pool is not None:
+            ops.reposition_kv_layers(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], out.copy_src,
+                                     out.copy_dst, out.copy_pairs, cos_sin)
+        host = {k: getattr(out, k).cpu().numpy() for k in
+                ("copy_src", "copy_dst", "copy_pairs", "released_pages", "page_table", "raw_indices",
+                 "active_positions")}
+        bases = inp.bases.cpu().numpy()
+        for j, b in enumerate(g):
+            got[b] = {
+                "copy_source_slots": host["copy_src"][bases[2, j] : bases[2, j + 1]],
+                "copy_destination_slots": host["copy_dst"][bases[2, j] : bases[2, j + 1]],
+                "copy_position_pairs": host["copy_pairs"][bases[2, j] : bases[2, j + 1]],
+                "released_pages": host["released_pages"][bases[5, j] : bases[5, j + 1]],
+                "page_table": host["page_table"][bases[4, j] : bases[4, j + 1]],
+                "raw_indices": host["raw_indices"][bases[1, j] : bases[1, j + 1]],
+                "active_positions": host["active_positions"][bases[1, j] : bases[1, j + 1]],
+            }
+    return got
+
+
+def _check_tables(w, a, layouts, got, table, order):
+    table_np = table.cpu().numpy()
+    for b, lay in enumerate(layouts):
+        want = pg.compact_pages(a.birth_rows[b], lay.keep_mask, lay.birth_positions, lay.positions,
+                                a.fresh_pages[b], w.page_size)
+        n = w.lengths[b]
+        np.testing.assert_array_equal(table_np[order[b], :n], want["terminal_row"], err_msg=f"row {b}")
+        assert (table_np[order[b], n:] == -7).all()
+        for key, value in got[b].items():
+            np.testing.assert_array_equal(value, np.asarray(want[key]).astype(value.dtype),
+                                          err_msg=f"{key} of request {b}")
+
+
+@pytest.mark.parametrize("groups", [None, "quarters"])
+def test_shared_prefix_cow_bit_exact(device, groups):
+    w = synth.workload("llama3-cow-small")
+    B = w.n_requests
+    split = None if groups is None else [range(i, i + 4) for i in range(0, B, 4)]
+    a = synth.assign_pages(w, split)
+    layouts = synth.compile_layouts(w)
+    P = w.page_size
+    pool = synth.make_pool(w.model, a.pool_pages * P, device, seed=4, generate_on_device=True)
+    cos_sin = synth.rope_table(w, device)
+    k_before = [t.clone() for t in pool.k]
+    v_before = [t.clone() for t in pool.v]
+    order = np.random.default_rng(0).permutation(B + 3)[:B]
+    table = _table_for(a.birth_rows, max(w.lengths) + 5, device, order)
+    print(f"cow: {B} requests, {a.pool_pages} pages, groups={len(a.groups)}", flush=True)
+    got = _run_groups(w, a, layouts, table, order, device, pool, cos_sin)
+    torch.cuda.synchronize()
+    _check_tables(w, a, layouts, got, table, order)
+
+    src = np.concatenate([got[b]["copy_source_slots"] for b in range(B)]).astype(np.int64)
+    dst = np.concatenate([got[b]["copy_destination_slots"] for b in range(B)]).astype(np.int64)
+    pairs = np.concatenate([got[b]["copy_position_pairs"] for b in range(B)])
+    assert len(np.unique(dst)) == len(dst)
+    src_d = torch.from_numpy(src).to(device)
+    dst_d = torch.from_numpy(dst).to(device)
+    untouched = torch.ones(a.pool_pages * P, dtype=torch.bool, device=device)
+    untouched[dst_d] = False
+    table_np = to_storage(cos_sin)
+    # the oracle's K check runs on a seeded sample of the copies (all of them
+    # would take minutes of CPU); unmoved-position copies are all in it
+    rng = np.random.default_rng(1)
+    same = np.flatnonzero(pairs[:, 0] == pairs[:, 1])
+    sample = np.union1d(rng.choice(len(src), size=min(len(src), 6000), replace=False), same)
+    s_src, s_dst = src_d[torch.from_numpy(sample).to(device)], dst_d[torch.from_numpy(sample).to(device)]
+    for l in range(w.model.n_layers):
+        # V bit for bit, every other slot (shared prefix pages included) unchanged
+        assert torch.equal(pool.v[l][dst_d].view(torch.int16), v_before[l][src_d].view(torch.int16))
+        assert torch.equal(pool.k[l][untouched].view(torch.int16), k_before[l][untouched].view(torch.int16))
+        assert torch.equal(pool.v[l][untouched].view(torch.int16), v_before[l][untouched].view(torch.int16))
+        # K against the oracle's two-step rotation
+        m = len(sample)
+        kk = [np.concatenate((to_storage(k_before[l][s_src]), np.zeros((m,) + pool.k[l].shape[1:], np.uint16)))]
+        vv = [np.zeros_like(kk[0])]
+        rp.reposition_kv_layers(kk, vv, np.arange(m), np.arange(m, 2 * m), pairs[sample], table_np, dtype="bf16")
+        assert storage_equal(to_storage(pool.k[l][s_dst]), kk[0][m:]), f"layer {l}"
+
+
+def _edge_workload():
+    # raggeds tails, a drop at token 0 (every page copied), a drop on a page
+    # boundary, one inside the last page, and a request with no drop at all
+    lengths = (37, 160, 100, 64, 33)
+    spans = (((0, 5),), ((32, 48), (50, 51)), ((97, 99),), (), ((16, 17),))
+    return synth.Workload("paged-edges", synth.TINY, lengths, spans, seed=12, table_positions=200,
+                          pool_slots=0, page_size=16, shared_prefix=0)
+
+
+def test_edge_requests(device):
+    w = _edge_workload()
+    a = synth.assign_pages(w)
+    layouts = synth.compile_layouts(w)
+    order = np.arange(w.n_requests) + 1
+    table = _table_for(a.birth_rows, 170, device, order)
+    got = _run_groups(w, a, layouts, table, order, device)
+    torch.cuda.synchronize()
+    _check_tables(w, a, layouts, got, table, order)
+    # no drop: nothing copied or released, page table unchanged
+    assert len(got[3]["copy_source_slots"]) == 0 and len(got[3]["released_pages"]) == 0
+    # drop at token 0: every page released, every kept token copied
+    assert len(got[0]["released_pages"]) == 3 and len(got[0]["copy_source_slots"]) == 32
+
+
+def test_row_pointers_and_birth_slots(device):
+    w = _edge_workload()
+    a = synth.assign_pages(w)
+    layouts = synth.compile_layouts(w)
+    B = w.n_requests
+    rows = [torch.from_numpy(np.concatenate((r, np.full(3, -7, np.int32)))).to(device) for r in a.birth_rows]
+    ptrs = torch.tensor([r.data_ptr() for r in rows], dtype=torch.int64, device=device)
+    dummy = torch.zeros((1, 1), dtype=torch.int32, device=device)
+    inp = tables.pack_paged_inputs(layouts, w.page_size, device)
+    out = tables.allocate_paged_outputs(inp, device)
+    fresh = torch.from_numpy(np.concatenate(a.fresh_pages).astype(np.int32)).to(device)
+    # birth slots given separately; the rows start out holding garbage
+    births = torch.from_numpy(np.concatenate(a.birth_rows)).to(device)
+    for r in rows:
+        r[:-3] = 12345
+    tables.compact_pages(inp, dummy, torch.arange(B, dtype=torch.int64, device=device), fresh, out,
+                         row_pointers=ptrs, birth_slots=births)
+    torch.cuda.synchronize()
+    for b, lay in enumerate(layouts):
+        want = pg.compact_pages(a.birth_rows[b], lay.keep_mask, lay.birth_positions, lay.positions,
+                                a.fresh_pages[b], w.page_size)
+        got = rows[b].cpu().numpy()
+        np.testing.assert_array_equal(got[:-3], want["terminal_row"])
+        assert (got[-3:] == -7).all()
+
+
+def test_page_one_matches_compact_rows(device):
+    case = synth.workload("tiny")
+    layouts = synth.compile_layouts(case)
+    slots = synth.assign_slots(case, layouts)
+    n = case.lengths[0]
+    # the row kernel
+    inp = tables.pack_compaction_inputs(layouts, device)
+    out = tables.allocate_outputs(inp, device)
+    t1 = torch.from_numpy(slots.birth_rows[0][None, :].copy()).to(device)
+    tables.compact_rows(inp, t1, torch.zeros(1, dtype=torch.int64, device=device),
+                        torch.from_numpy(slots.fresh[0]).to(device), out)
+    # the page kernel with P = 1 and the same fresh slots as pages
+    pin = tables.pack_paged_inputs(layouts, 1, device)
+    assert pin.fresh_pages == (len(slots.fresh[0]),)
+    pout = tables.allocate_paged_outputs(pin, device)
+    t2 = torch.from_numpy(slots.birth_rows[0][None, :].copy()).to(device)
+    tables.compact_pages(pin, t2, torch.zeros(1, dtype=torch.int64, device=device),
+                         torch.from_numpy(slots.fresh[0]).to(device), pout)
+    torch.cuda.synchronize()
+    assert torch.equal(t1, t2)
+    assert torch.equal(out.copy_src, pout.copy_src)
+    assert torch.equal(out.copy_dst, pout.copy_dst)
+    assert torch.equal(out.copy_pairs, pout.copy_pairs)
+    assert torch.equal(out.retired, pout.released_pages)
+    assert torch.equal(out.raw_indices, pout.raw_indices)
+    assert torch.equal(out.active_positions, pout.active_positions)
+    assert n == t1.shape[1]
