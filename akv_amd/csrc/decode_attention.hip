@@ -215,29 +215,62 @@ __global__ void __launch_bounds__(64) decode_attention_partial_kernel(const Attn
 }
 
 // One workgroup per (request, q head): merge chunk partials and the sink.
+// kWays groups of D threads each fold every kWays-th chunk with an online
+// (max, sum) merge -- the loads of one chunk do not wait on the previous
+// one -- and the groups meet in LDS.
+constexpr int kWays = 4;
+
 template <int D>
-__global__ void __launch_bounds__(D) decode_attention_combine_kernel(const AttnArgs a) {
+__global__ void __launch_bounds__(kWays * D) decode_attention_combine_kernel(const AttnArgs a) {
+  __shared__ float s_m[kWays], s_l[kWays];
+  __shared__ float s_o[kWays][D];
   const int b = blockIdx.x;
   const int h = blockIdx.y;
   const int g = h / a.group;
   const int hl = h - g * a.group;
-  const int d = threadIdx.x;
+  const int d = threadIdx.x % D;
+  const int way = threadIdx.x / D;
   const int64_t len = a.kv_indptr[b + 1] - a.kv_indptr[b];
-  const int used = static_cast<int>((len + kChunk - 1) / kChunk);
+  // keys past max_len (a caller error) are not read: the partials stop there
+  const int64_t want = (len + kChunk - 1) / kChunk;
+  const int used = static_cast<int>(want < a.chunks ? want : a.chunks);
   const float* base = a.partial + (static_cast<int64_t>(b) * a.kv_heads + g) * a.chunks * 16 * (D + 2);
-  float m = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
-  for (int c = 0; c < used; ++c) m = fmaxf(m, base[(c * 16 + hl) * (D + 2) + D]);
-  float l = (a.sinks && m != -INFINITY) ? exp2f(a.sinks[h] * kLog2e - m) : 0.f;
-  float o = 0.f;
-  for (int c = 0; c < used; ++c) {
+  float m = -INFINITY, l = 0.f, o = 0.f;
+#pragma unroll 4
+  for (int c = way; c < used; c += kWays) {
     const float* pc = base + (c * 16 + hl) * (D + 2);
     const float mc = pc[D];
-    if (mc == -INFINITY) continue;
-    const float w = exp2f(mc - m);
-    l += pc[D + 1] * w;
-    o += pc[d] * w;
+    const float lc = pc[D + 1];
+    const float oc = pc[d];
+    // an empty chunk carries m = -inf and no o values
+    const bool valid = mc != -INFINITY;
+    const float mn = valid ? fmaxf(m, mc) : m;
+    const float ws = valid ? exp2f(m - mn) : 1.f;
+    const float wc = valid ? exp2f(mc - mn) : 0.f;
+    l = l * ws + (valid ? lc : 0.f) * wc;
+    o = o * ws + (valid ? oc : 0.f) * wc;
+    m = mn;
   }
-  const float r = l > 0.f ? o / l : 0.f;
+  s_o[way][d] = o;
+  if (d == 0) {
+    s_m[way] = m;
+    s_l[way] = l;
+  }
+  __syncthreads();
+  if (way != 0) return;
+  float mt = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kWays; ++w) mt = fmaxf(mt, s_m[w]);
+  float lt = (a.sinks && mt != -INFINITY) ? exp2f(a.sinks[h] * kLog2e - mt) : 0.f;
+  float ot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWays; ++w) {
+    if (s_m[w] == -INFINITY) continue;
+    const float sw = exp2f(s_m[w] - mt);
+    lt += s_l[w] * sw;
+    ot += s_o[w][d] * sw;
+  }
+  const float r = lt > 0.f ? ot / lt : 0.f;
   const int64_t at = static_cast<int64_t>(b) * a.out_stride_b + static_cast<int64_t>(h) * a.out_stride_h + d;
   if (a.out_f32)
     static_cast<float*>(a.out)[at] = r;
@@ -318,12 +351,14 @@ extern "C" int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q
     hipLaunchKernelGGL(decode_attention_partial_kernel<64>, grid, block, 0, st, a);
     int rc = check_launch("akv_decode_attention (partial)");
     if (rc) return rc;
-    hipLaunchKernelGGL(decode_attention_combine_kernel<64>, dim3(n_requests, q_heads), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(decode_attention_combine_kernel<64>, dim3(n_requests, q_heads), dim3(kWays * 64), 0, st,
+                       a);
   } else {
     hipLaunchKernelGGL(decode_attention_partial_kernel<128>, grid, block, 0, st, a);
     int rc = check_launch("akv_decode_attention (partial)");
     if (rc) return rc;
-    hipLaunchKernelGGL(decode_attention_combine_kernel<128>, dim3(n_requests, q_heads), dim3(128), 0, st, a);
+    hipLaunchKernelGGL(decode_attention_combine_kernel<128>, dim3(n_requests, q_heads), dim3(kWays * 128), 0,
+                       st, a);
   }
   return check_launch("akv_decode_attention (combine)");
 }

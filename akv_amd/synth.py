@@ -290,7 +290,13 @@ class SlotAssignment:
     moved: list  # per request: number of moved tokens
 
 
-def assign_slots(w, layouts):
+def assign_slots(w, layouts, order="permutation"):
+    """Birth and fresh slots.  ``order="permutation"``: a seeded random
+    permutation of the free slots (a fragmented pool, the worst case for the
+    Reposition's row accesses); ``"ascending"``: the free list in ascending
+    order, what a page-one allocator hands out from an unfragmented pool."""
+    if order not in ("permutation", "ascending"):
+        raise ValueError(f"unknown slot order {order!r}")
     rng = np.random.default_rng(w.seed + 1000)
     total = sum(w.lengths)
     moved = [int((np.asarray(l.keep_mask) & (np.asarray(l.birth_positions) != np.asarray(l.positions))).sum())
@@ -298,7 +304,8 @@ def assign_slots(w, layouts):
     need = total + sum(moved)
     if need + 1 > w.pool_slots:
         raise ValueError("pool too small for the workload")
-    perm = rng.permutation(np.arange(1, w.pool_slots, dtype=np.int64)).astype(np.int32)
+    free = np.arange(1, w.pool_slots, dtype=np.int64)
+    perm = (rng.permutation(free) if order == "permutation" else free).astype(np.int32)
     births, fresh, at = [], [], 0
     for n in w.lengths:
         births.append(perm[at : at + n])

@@ -45,6 +45,7 @@ def parse_args():
     p.add_argument("--latency-iters", type=int, default=100)
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-cow", action="store_true", help="skip the page-16 copy-on-write configuration")
     p.add_argument("--reposition-only", action="store_true",
                    help="time only the Reposition launch (for profiling runs)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -62,7 +63,7 @@ def copy_calibration(device):
 
 
 class Pipeline:
-    def __init__(self, name, device):
+    def __init__(self, name, device, slot_order="permutation"):
         self.device = device
         w = self.w = synth.workload(name)
         if w.n_requests != 1:
@@ -72,7 +73,7 @@ class Pipeline:
         self.layouts = synth.compile_layouts(w)
         self.compile_s = time.perf_counter() - t0
         lay = self.layouts[0]
-        slots = synth.assign_slots(w, self.layouts)
+        slots = synth.assign_slots(w, self.layouts, slot_order)
         self.slots = slots
         n = w.lengths[0]
         self.n = n
@@ -180,6 +181,23 @@ def tiny_config(device, flush):
     }
 
 
+def ascending_slots_config(device, flush):
+    """The 32k GPT-OSS step with slots from an unfragmented ascending free
+    list instead of a random permutation: same tokens, spans and bytes."""
+    pipe = Pipeline("gpt-oss-32k", device, slot_order="ascending")
+    warm, cold = _time_steps(pipe.step, 50, 10, 50, flush)
+    repo_warm, _ = _time_steps(pipe.reposition, 50, 10, 0, flush)
+    out = {
+        "workload": pipe.w.name + ", ascending slots", "moved": pipe.moved,
+        "step_ms_back_to_back": round(warm, 5), "step_p50_ms": round(percentile(cold, 50), 5),
+        "retained_kv_GBs": round(pipe.retained_bytes / (warm / 1e3) / 1e9, 1),
+        "reposition_ms": round(repo_warm, 5),
+        "reposition_pct_hbm_peak": round(100 * pipe.alg_bytes / (repo_warm / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
+    }
+    del pipe
+    return out
+
+
 def ragged_config(device, flush):
     """64 requests of 2k-64k tokens: batched compaction + kv_indptr / kv_indices / last-page rebuild."""
     w = synth.workload("ragged-64")
@@ -278,6 +296,82 @@ def decode_consumer_config(device, flush):
         "full_layer_kv_GBs": round(kv_bytes / (warm_full / 1e3) / 1e9, 1),
         "window128_layer_ms": round(warm_win, 5), "window128_layer_p50_ms": round(percentile(cold_win, 50), 5),
         "kernel_launches_per_layer": 2,
+    }
+
+
+def cow_config(device, flush):
+    """Llama-3-8B page-16 copy-on-write: 16 requests over a shared 8192-token
+    prefix with 16k-120k private suffixes.  Requests run in the fewest groups
+    whose pool (old pages + the fresh pages not covered by pages the earlier
+    groups released) fits the free HBM; per group one paged compaction and
+    one all-layer Reposition."""
+    w = synth.workload("llama3-cow-16")
+    m = w.model
+    P = w.page_size
+    t0 = time.perf_counter()
+    layouts = synth.compile_layouts(w)
+    compile_ms = (time.perf_counter() - t0) * 1e3
+    torch.cuda.empty_cache()
+    free, _ = torch.cuda.mem_get_info(device)
+    page_bytes = P * m.n_layers * m.n_heads * m.head_dim * 2 * 2
+    assignment = None
+    for n_groups in (1, 2, 4, 8, 16):
+        size = w.n_requests // n_groups
+        a = synth.assign_pages(w, [range(i, i + size) for i in range(0, w.n_requests, size)])
+        if a.pool_pages * page_bytes < free - (12 << 30):
+            assignment = a
+            break
+    if assignment is None:
+        return {"workload": w.name, "skipped": f"pool does not fit {free / 2**30:.0f} GiB of free HBM"}
+    a = assignment
+    pool = synth.make_pool(m, a.pool_pages * P, device, seed=4, generate_on_device=True)
+    rope = synth.rope_table(w, device)
+    table = torch.full((w.n_requests, max(w.lengths) + 8), -1, dtype=torch.int32, device=device)
+    groups = []
+    for g in a.groups:
+        g = list(g)
+        inp = tables.pack_paged_inputs([layouts[b] for b in g], P, device)
+        groups.append(dict(
+            inputs=inp, out=tables.allocate_paged_outputs(inp, device),
+            rows=torch.tensor(g, dtype=torch.int64, device=device),
+            fresh=torch.from_numpy(np.concatenate([a.fresh_pages[b] for b in g])).to(device),
+            birth=torch.from_numpy(np.concatenate([a.birth_rows[b] for b in g])).to(device),
+            events=[],
+        ))
+    copies = sum(sum(gr["inputs"].copies) for gr in groups)
+
+    def step(record=False):
+        for gr in groups:
+            tables.compact_pages(gr["inputs"], table, gr["rows"], gr["fresh"], gr["out"], birth_slots=gr["birth"])
+            o = gr["out"]
+            if record:
+                e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                e[0].record()
+            ops.reposition_kv_layers(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], o.copy_src, o.copy_dst,
+                                     o.copy_pairs, rope)
+            if record:
+                e[1].record()
+                gr["events"].append(e)
+
+    warm, cold = _time_steps(step, 10, 2, 5, flush)
+    for gr in groups:
+        gr["events"].clear()
+    step(record=True)
+    step(record=True)
+    torch.cuda.synchronize()
+    repo_ms = sum(float(np.mean([b.elapsed_time(e) for b, e in gr["events"]])) for gr in groups)
+    retained = copies * 4 * m.n_layers * m.n_heads * m.head_dim * 2
+    alg = retained + copies * 16 + copies * 2 * m.rotary_dim * 4
+    del pool
+    torch.cuda.empty_cache()
+    return {
+        "workload": w.name, "requests": w.n_requests, "tokens": sum(w.lengths), "copies": copies,
+        "page_size": P, "groups": len(a.groups), "pool_GiB": round(a.pool_pages * page_bytes / 2**30, 1),
+        "step_ms_back_to_back": round(warm, 4), "step_p50_ms": round(percentile(cold, 50), 4),
+        "retained_kv_GBs": round(retained / (warm / 1e3) / 1e9, 1),
+        "reposition_ms_per_step": round(repo_ms, 4),
+        "reposition_pct_hbm_peak": round(100 * alg / (repo_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
+        "kernel_launches_per_step": 2 * len(a.groups), "host_event_compile_ms": round(compile_ms, 1),
     }
 
 
@@ -484,8 +578,11 @@ def main():
     }
     if not args.reposition_only:
         print("# secondary configurations ...", file=sys.stderr, flush=True)
-        result["other_configs"] = [tiny_config(device, pipe.flush), ragged_config(device, pipe.flush),
-                                   decode_consumer_config(device, pipe.flush)]
+        result["other_configs"] = [tiny_config(device, pipe.flush), ascending_slots_config(device, pipe.flush),
+                                   ragged_config(device, pipe.flush), decode_consumer_config(device, pipe.flush)]
+        if not args.no_cow:
+            print("# copy-on-write configuration ...", file=sys.stderr, flush=True)
+            result["other_configs"].append(cow_config(device, pipe.flush))
     if not args.no_cpu_baseline:
         print("# cpu baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(pipe, args.cpu_seconds)

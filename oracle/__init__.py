@@ -25,6 +25,13 @@ reference repository root):
                 (``akv/system/sglang/kernels/ops/attention/context_page_table.py:7-76``),
                 ``write_row_slots`` (``.../ops/memory/context_rows.py:7-15``) and the
                 ``kv_indptr = cumsum`` rebuild (``akv/system/sglang.patch:2266-2268``).
+``attention``   one GQA decode step with attention sinks, the consumer of the
+                compacted metadata (sink normalisation of
+                ``akv/system/sglang/srt/layers/attention/context_backend.py:254-272``).
+``paging``      page-granular Drop + Reposition with copy-on-write; the
+                reference rejects page sizes other than 1
+                (``context_reposition.py:153-154``), so this module is the
+                extension's specification, pinned to ``occurrence`` at page size 1.
 
 How each function is pinned (golden vectors / closed forms / brute force /
 invariants) is stated in its module docstring.  The RoPE tables are not part

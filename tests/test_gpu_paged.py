@@ -6,6 +6,8 @@ pages; shared prefix pages and every other slot left untouched.  With page
 size 1 the paged kernel reproduces ``akv_compact_rows``.
 """
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -71,9 +73,12 @@ def _check_tables(w, a, layouts, got, table, order):
                                           err_msg=f"{key} of request {b}")
 
 
-@pytest.mark.parametrize("groups", [None, "quarters"])
-def test_shared_prefix_cow_bit_exact(device, groups):
-    w = synth.workload("llama3-cow-small")
+@pytest.mark.parametrize("name,groups", [("llama3-cow-small", None), ("llama3-cow-small", "quarters"),
+                                         ("llama3-cow-16", "quarters")])
+def test_shared_prefix_cow_bit_exact(device, name, groups):
+    # the full-size workload keeps every token count and page of the 16
+    # requests but 2 of the 32 layers (a 13 GiB pool instead of 214 GiB)
+    w = dataclasses.replace(synth.workload(name), model=synth.LLAMA3_8B_2L)
     B = w.n_requests
     split = None if groups is None else [range(i, i + 4) for i in range(0, B, 4)]
     a = synth.assign_pages(w, split)
