@@ -62,6 +62,12 @@ _SIGNATURES = {
          c_int32, c_int32, _P, _P, _P, ctypes.c_float, _P, c_int32, c_int64, c_int64, c_int64,
          _P, c_int64, _P],
     ),
+    "akv_context_attention": (
+        c_int32,
+        [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64,
+         c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, _P, _P, c_int32, _P, c_int32, _P, _P,
+         c_int32, c_int32, _P, ctypes.c_float, _P, c_int32, c_int64, c_int64, c_int64, _P],
+    ),
     "akv_plan_count": (
         c_int32,
         [c_int64, _P, c_int64, _P, _P, c_int64, _P, _P, c_int64, _P, _P],

@@ -239,6 +239,42 @@ int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                          int64_t workspace_bytes, void* stream);
 
 /*
+ * Prefill context attention over occurrence metadata (MFMA, bf16 in, fp32
+ * accumulate).  Segment s: queries q[qo_indptr[s] .. qo_indptr[s+1]) with
+ * their own keys k_ext/v_ext (causal by index) after the prefix keys
+ * kv_indices[kv_indptr[s] .. kv_indptr[s+1]) of the pool (all visible);
+ * with sliding_window >= 0 a key is visible only if q_pos <= k_pos + window,
+ * positions from q_positions / kv_positions (both or neither; without them
+ * q_pos = prefix_len + i, k_pos = j).  Positions ascend within a segment.
+ * sinks (opt.) f32 [q_heads] add e^sink to the softmax denominator.
+ * q [Nq, q_heads, D], k_ext/v_ext [Nq, kv_heads, D], pool [slots, kv_heads, D]
+ * bf16 with unit dim stride; out bf16 or f32 like q; D = 64 or 128;
+ * q_heads / kv_heads divides 128.  indptrs / indices / positions: AKV_I32
+ * or AKV_I64.  max_query_len: host bound on every segment's query count.
+ * Replaces the Triton extend attention launched by
+ * ContextAttentionMetadata.forward with context positions,
+ * akv/system/sglang/srt/layers/attention/context_backend.py:180-251 and
+ * akv/system/sglang.patch:106-237 (extend_attention_fwd).
+ */
+int akv_context_attention(const void* q, int64_t q_stride_t,
+                          int64_t q_stride_h, const void* k_ext,
+                          const void* v_ext, int64_t k_ext_stride_t,
+                          int64_t k_ext_stride_h, int64_t v_ext_stride_t,
+                          int64_t v_ext_stride_h, const void* k_buffer,
+                          const void* v_buffer, int64_t k_stride_slot,
+                          int64_t k_stride_head, int64_t v_stride_slot,
+                          int64_t v_stride_head, int32_t n_segments,
+                          int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                          const void* qo_indptr, const void* kv_indptr,
+                          int32_t indptr_dtype, const void* kv_indices,
+                          int32_t indices_dtype, const void* q_positions,
+                          const void* kv_positions, int32_t positions_dtype,
+                          int32_t sliding_window, const float* sinks,
+                          float scale, void* out, int32_t out_dtype,
+                          int64_t out_stride_t, int64_t out_stride_h,
+                          int64_t max_query_len, void* stream);
+
+/*
  * Host event compiler (CPU, no device work).  Replays Drop and Reposition
  * events over the raw token stream.  Two calls, like the reference's count
  * and fill passes: akv_plan_count returns the number of transitions through

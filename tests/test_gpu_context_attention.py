@@ -1,0 +1,109 @@
+"""GPU parity of the prefill context attention (MFMA) against the float64
+oracle: ragged segments, empty and long prefixes, GQA groups 8 and 4, head
+dims 64 and 128, position-based sliding windows over positions with holes,
+the native (position-free) window, sinks, bf16 and f32 outputs; and the
+metadata path (ContextSequence -> plan -> bind -> forward)."""
+
+import numpy as np
+import pytest
+import torch
+
+from akv_amd import context_attention as ca
+from oracle import attention as oat
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2  # abs, bf16 inputs and P in bf16 (the decode check's tolerance)
+
+
+def _f32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _case(device, hq, hkv, d, q_lens, p_lens, seed, slots=4000):
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    nq = sum(q_lens)
+    q = torch.randn((nq, hq, d), generator=g).to(torch.bfloat16)
+    ke = torch.randn((nq, hkv, d), generator=g).to(torch.bfloat16)
+    ve = torch.randn((nq, hkv, d), generator=g).to(torch.bfloat16)
+    kp = torch.randn((slots, hkv, d), generator=g).to(torch.bfloat16)
+    vp = torch.randn((slots, hkv, d), generator=g).to(torch.bfloat16)
+    qo = np.concatenate(([0], np.cumsum(q_lens))).astype(np.int64)
+    kv = np.concatenate(([0], np.cumsum(p_lens))).astype(np.int64)
+    idx = rng.integers(1, slots, size=kv[-1]).astype(np.int32)
+    # ordered positions with holes: prefix first, then the queries
+    kpos, qpos = [], []
+    for n, p in zip(q_lens, p_lens):
+        allp = np.sort(rng.choice(4 * (n + p) + 8, size=n + p, replace=False))
+        kpos.append(allp[:p])
+        qpos.append(allp[p:])
+    kpos = np.concatenate(kpos).astype(np.int64)
+    qpos = np.concatenate(qpos).astype(np.int64)
+    dev = {k: v.to(device) for k, v in dict(q=q, ke=ke, ve=ve, kp=kp, vp=vp).items()}
+    return dict(q=q, ke=ke, ve=ve, kp=kp, vp=vp, qo=qo, kv=kv, idx=idx, kpos=kpos, qpos=qpos, dev=dev)
+
+
+def _run(device, c, *, window, positions, sinks, out_dtype, scale):
+    dv = c["dev"]
+    out = torch.full(dv["q"].shape, 7.0, dtype=out_dtype, device=device)
+    qo = torch.from_numpy(c["qo"]).to(device)
+    kv = torch.from_numpy(c["kv"]).to(device)
+    idx = torch.from_numpy(c["idx"]).to(device)
+    qp = torch.from_numpy(c["qpos"]).to(device) if positions else None
+    kp = torch.from_numpy(c["kpos"]).to(device) if positions else None
+    ca.extend_attention_fwd(dv["q"], dv["ke"], dv["ve"], out, dv["kp"], dv["vp"], qo, kv, idx, None, True, None,
+                            int(np.diff(c["qo"]).max()), sm_scale=scale, sliding_window_size=window, sinks=sinks,
+                            context_q_positions=qp, context_kv_positions=kp)
+    torch.cuda.synchronize()
+    want = oat.context_attention(_f32(c["q"]), _f32(c["ke"]), _f32(c["ve"]), _f32(c["kp"]), _f32(c["vp"]),
+                                 c["qo"], c["kv"], c["idx"], scale, window=window,
+                                 q_positions=c["qpos"] if positions else None,
+                                 kv_positions=c["kpos"] if positions else None,
+                                 sinks=_f32(sinks) if sinks is not None else None)
+    return _f32(out), want
+
+
+Q_LENS = [1, 15, 16, 17, 100, 300, 5]
+P_LENS = [0, 5, 64, 1000, 0, 37, 130]
+
+
+@pytest.mark.parametrize("d,hq,hkv", [(64, 64, 8), (128, 32, 8)])
+@pytest.mark.parametrize("window,positions", [(-1, False), (24, True), (24, False)])
+@pytest.mark.parametrize("with_sinks", [True, False])
+def test_segments_match_oracle(device, d, hq, hkv, window, positions, with_sinks):
+    c = _case(device, hq, hkv, d, Q_LENS, P_LENS, seed=d + hq + window + with_sinks)
+    sinks = (torch.randn(hq, generator=torch.Generator().manual_seed(1)) * 2).to(device) if with_sinks else None
+    print(f"context attention d={d} hq={hq} window={window} positions={positions} sinks={with_sinks}", flush=True)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        got, want = _run(device, c, window=window, positions=positions, sinks=sinks, out_dtype=out_dtype,
+                         scale=d ** -0.5)
+        for s in range(len(Q_LENS)):
+            a, b = c["qo"][s], c["qo"][s + 1]
+            err = np.abs(got[a:b] - want[a:b]).max()
+            assert err <= TOL, f"segment {s} (q {Q_LENS[s]}, prefix {P_LENS[s]}) max err {err}"
+
+
+def test_metadata_path_ordinary_sequences(device):
+    """ContextSequence.ordinary -> ContextAttentionPlan.merge/bind -> forward."""
+    hq, hkv, d = 64, 8, 64
+    seqs = [ca.ContextSequence.ordinary(37, 20), ca.ContextSequence.ordinary(0, 70),
+            ca.ContextSequence.ordinary(300, 1)]
+    plan = ca.ContextAttentionPlan.merge(seqs)
+    rng = np.random.default_rng(0)
+    slots = torch.from_numpy(rng.permutation(np.arange(1, 1 + plan.occurrence_count)).astype(np.int64)).to(device)
+    meta = plan.bind(slots)
+    g = torch.Generator().manual_seed(2)
+    nq = meta.query_count
+    q = torch.randn((nq, hq, d), generator=g).to(torch.bfloat16).to(device)
+    ke = torch.randn((nq, hkv, d), generator=g).to(torch.bfloat16).to(device)
+    ve = torch.randn((nq, hkv, d), generator=g).to(torch.bfloat16).to(device)
+    pool_k = torch.randn((plan.occurrence_count + 1, hkv, d), generator=g).to(torch.bfloat16).to(device)
+    pool_v = torch.randn((plan.occurrence_count + 1, hkv, d), generator=g).to(torch.bfloat16).to(device)
+    out = torch.empty_like(q)
+    meta.forward(ca.extend_attention_fwd, q, ke, ve, out, pool_k, pool_v, sliding_window_size=-1)
+    torch.cuda.synchronize()
+    qo, kv, occ, qpos, kpos = meta.cpu_fields
+    want = oat.context_attention(_f32(q), _f32(ke), _f32(ve), _f32(pool_k), _f32(pool_v), qo, kv,
+                                 slots.cpu().numpy()[occ], d ** -0.5, q_positions=qpos, kv_positions=kpos)
+    assert np.abs(_f32(out) - want).max() <= TOL

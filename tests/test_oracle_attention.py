@@ -43,3 +43,96 @@ def test_single_key_closed_form():
     want = v[0, 0] * np.exp(s) / (np.exp(s) + np.exp(0.3))
     np.testing.assert_allclose(at.decode_attention(q, k, v, 1.0, np.array([0.3]))[0], want, rtol=1e-6)
     assert np.all(at.decode_attention(q, k[:0], v[:0], 1.0, np.array([0.3])) == 0)
+
+
+def _segments(rng, hq, hkv, d, q_lens, p_lens, slots=300):
+    nq = sum(q_lens)
+    q = rng.standard_normal((nq, hq, d)).astype(np.float32)
+    ke = rng.standard_normal((nq, hkv, d)).astype(np.float32)
+    ve = rng.standard_normal((nq, hkv, d)).astype(np.float32)
+    kp = rng.standard_normal((slots, hkv, d)).astype(np.float32)
+    vp = rng.standard_normal((slots, hkv, d)).astype(np.float32)
+    qo = np.concatenate(([0], np.cumsum(q_lens)))
+    kv = np.concatenate(([0], np.cumsum(p_lens)))
+    idx = rng.integers(0, slots, size=kv[-1])
+    return q, ke, ve, kp, vp, qo, kv, idx
+
+
+def _sdpa(q, k, v, mask, scale):
+    """q [n, hq, d], k/v [m, hkv, d], mask [n, m] -> [n, hq, d] via torch SDPA (fp64)."""
+    hq, hkv = q.shape[1], k.shape[1]
+    qq = torch.from_numpy(q.astype(np.float64)).permute(1, 0, 2)
+    kk = torch.from_numpy(k.astype(np.float64)).permute(1, 0, 2).repeat_interleave(hq // hkv, 0)
+    vv = torch.from_numpy(v.astype(np.float64)).permute(1, 0, 2).repeat_interleave(hq // hkv, 0)
+    o = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv, attn_mask=torch.from_numpy(mask), scale=scale)
+    return o.permute(1, 0, 2).numpy()
+
+
+def test_context_no_prefix_is_causal_sdpa():
+    rng = np.random.default_rng(3)
+    hq, hkv, d = 8, 2, 16
+    q, ke, ve, kp, vp, qo, kv, idx = _segments(rng, hq, hkv, d, [5, 1, 12], [0, 0, 0])
+    got = at.context_attention(q, ke, ve, kp, vp, qo, kv, idx, 0.25)
+    for s in range(3):
+        a, b = qo[s], qo[s + 1]
+        qq = torch.from_numpy(q[a:b].astype(np.float64)).permute(1, 0, 2)
+        kk = torch.from_numpy(ke[a:b].astype(np.float64)).permute(1, 0, 2).repeat_interleave(4, 0)
+        vv = torch.from_numpy(ve[a:b].astype(np.float64)).permute(1, 0, 2).repeat_interleave(4, 0)
+        want = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv, is_causal=True, scale=0.25)
+        np.testing.assert_allclose(got[a:b], want.permute(1, 0, 2).numpy(), atol=1e-6, rtol=1e-5)
+
+
+def test_context_prefix_plus_causal_mask():
+    rng = np.random.default_rng(4)
+    hq, hkv, d = 4, 4, 8
+    q, ke, ve, kp, vp, qo, kv, idx = _segments(rng, hq, hkv, d, [7, 3], [10, 4])
+    got = at.context_attention(q, ke, ve, kp, vp, qo, kv, idx, 0.3)
+    for s in range(2):
+        a, b, x, y = qo[s], qo[s + 1], kv[s], kv[s + 1]
+        n, p = b - a, y - x
+        mask = np.zeros((n, p + n), dtype=bool)
+        mask[:, :p] = True
+        mask[:, p:] = np.tril(np.ones((n, n), dtype=bool))
+        want = _sdpa(q[a:b], np.concatenate((kp[idx[x:y]], ke[a:b])), np.concatenate((vp[idx[x:y]], ve[a:b])),
+                     mask, 0.3)
+        np.testing.assert_allclose(got[a:b], want, atol=1e-6, rtol=1e-5)
+
+
+def test_context_window_matches_searchsorted_gather():
+    # positions with holes (dropped spans): the reference's native plan finds
+    # each query's first visible key by searchsorted over the ordered positions
+    rng = np.random.default_rng(5)
+    hq, hkv, d, W = 4, 2, 8, 6
+    q_lens, p_lens = [9, 4], [12, 0]
+    q, ke, ve, kp, vp, qo, kv, idx = _segments(rng, hq, hkv, d, q_lens, p_lens)
+    kpos = np.concatenate([np.sort(rng.choice(40, size=n, replace=False)) for n in p_lens])
+    qpos = np.concatenate([50 + np.sort(rng.choice(30, size=n, replace=False)) for n in q_lens])
+    qpos[9:] = np.sort(rng.choice(20, size=4, replace=False))
+    got = at.context_attention(q, ke, ve, kp, vp, qo, kv, idx, 0.5, window=W, q_positions=qpos,
+                               kv_positions=kpos)
+    for s in range(2):
+        a, b, x, y = qo[s], qo[s + 1], kv[s], kv[s + 1]
+        positions = np.r_[kpos[x:y], qpos[a:b]]
+        keys_k = np.concatenate((kp[idx[x:y]], ke[a:b]))
+        keys_v = np.concatenate((vp[idx[x:y]], ve[a:b]))
+        for i in range(b - a):
+            end = y - x + i + 1
+            start = np.searchsorted(positions[:end], qpos[a + i] - W)
+            mask = np.ones((1, end - start), dtype=bool)
+            want = _sdpa(q[a + i : a + i + 1], keys_k[start:end], keys_v[start:end], mask, 0.5)
+            np.testing.assert_allclose(got[a + i], want[0], atol=1e-6, rtol=1e-5)
+
+
+def test_context_sinks_scale_by_sigmoid_of_lse():
+    rng = np.random.default_rng(6)
+    hq, hkv, d = 4, 1, 8
+    q, ke, ve, kp, vp, qo, kv, idx = _segments(rng, hq, hkv, d, [6], [5])
+    sinks = rng.standard_normal(hq).astype(np.float32)
+    base = at.context_attention(q, ke, ve, kp, vp, qo, kv, idx, 0.4)
+    got = at.context_attention(q, ke, ve, kp, vp, qo, kv, idx, 0.4, sinks=sinks)
+    keys = np.concatenate((kp[idx], ke)).astype(np.float64)
+    for i in range(6):
+        s = 0.4 * np.einsum("nd,hd->hn", keys[: 5 + i + 1, 0, :], q[i].astype(np.float64))
+        lse = torch.logsumexp(torch.from_numpy(s), dim=1).numpy()
+        want = base[i] * torch.sigmoid(torch.from_numpy(lse - sinks)).numpy()[:, None]
+        np.testing.assert_allclose(got[i], want, atol=1e-6, rtol=1e-5)
