@@ -47,29 +47,28 @@ constexpr int kRows = 128;  // (token, head) rows per workgroup
 constexpr int kThreads = 256;
 constexpr int kKeys = 64;  // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 8.f;  // log2-domain slack before the running maximum moves
 
 struct CtxArgs {
   const __bf16* q;
-  int64_t q_st, q_sh;
   const __bf16* k_ext;
   const __bf16* v_ext;
-  int64_t ke_st, ke_sh, ve_st, ve_sh;
   const __bf16* k_pool;
   const __bf16* v_pool;
-  int64_t kp_ss, kp_sh, vp_ss, vp_sh;
   const void* qo_indptr;
   const void* kv_indptr;
   const void* kv_indices;
   const void* q_pos;
   const void* kv_pos;
-  int32_t indptr_i64, indices_i64, pos_i64;
-  int32_t window;
   const float* sinks;
-  float scale_log2;
   void* out;
+  // element strides (checked to fit 32 bits on the host)
+  int32_t q_st, q_sh, ke_st, ke_sh, ve_st, ve_sh, kp_ss, kp_sh, vp_ss, vp_sh, o_st, o_sh;
+  int32_t indptr_i64;
+  int32_t window;
+  float scale_log2;
   int32_t out_f32;
-  int64_t o_st, o_sh;
-  int32_t kv_heads, group, tokens_per_block;
+  int32_t group, tokens_per_block;
 };
 
 __device__ __forceinline__ u32x4 load16(const __bf16* p) {
@@ -78,18 +77,24 @@ __device__ __forceinline__ u32x4 load16(const __bf16* p) {
 
 template <int D>
 struct Smem {
-  __bf16 k[2][kKeys][D + 8];       // key-major K tile, rows padded by 16 B
-  __bf16 vt[2][D][kKeys + 4];      // dim-major V tile, rows padded by 8 B
-  int64_t pos[2][kKeys];           // key positions
+  __bf16 k[2][kKeys][D + 8];   // key-major K tile, rows padded by 16 B
+  __bf16 vt[2][D][kKeys + 4];  // dim-major V tile, rows padded by 8 B
+  int32_t pos[2][kKeys];       // key positions relative to the block's first query
 };
 
-template <int D>
+constexpr int32_t kFar = 1 << 30;  // relative positions are clamped to [-kFar, kFar]
+
+__device__ __forceinline__ int32_t rel_pos(int64_t p, int64_t base) {
+  const int64_t r = p - base;
+  return static_cast<int32_t>(r < -kFar ? -kFar : (r > kFar ? kFar : r));
+}
+
+template <int D, typename IdxT, typename PosT, bool POS>
 __global__ void __launch_bounds__(kThreads) context_attention_kernel(const CtxArgs a) {
-  constexpr int kChunks = D / 8;                          // 16 B chunks per key row
-  constexpr int kKLoads = kKeys * kChunks / kThreads;     // K chunks per thread
-  constexpr int kVLoads = (kKeys / 2) * kChunks / kThreads;  // V key-pair chunks per thread
-  constexpr int kKSteps = D / 32;                         // MFMA k-steps over head dims
-  constexpr int kDTiles = D / 16;                         // O^T row tiles
+  constexpr int kChunks = D / 8;               // 16 B chunks per key row
+  constexpr int kRounds = kChunks / 8;         // (key pair, chunk) items per thread
+  constexpr int kKSteps = D / 32;              // MFMA k-steps over head dims
+  constexpr int kDTiles = D / 16;              // O^T row tiles
   __shared__ __attribute__((aligned(16))) Smem<D> sm;
 
   const int tid = threadIdx.x;
@@ -101,144 +106,156 @@ __global__ void __launch_bounds__(kThreads) context_attention_kernel(const CtxAr
   const int g = blockIdx.y;
   const bool i64 = a.indptr_i64;
   const int64_t qo0 = load_index(a.qo_indptr, i64, seg);
-  const int64_t qlen = load_index(a.qo_indptr, i64, seg + 1) - qo0;
+  const int32_t qlen = static_cast<int32_t>(load_index(a.qo_indptr, i64, seg + 1) - qo0);
   const int G = a.group;
   const int T = a.tokens_per_block;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * T;
+  const int32_t t0 = static_cast<int32_t>(blockIdx.x) * T;
   if (t0 >= qlen) return;
   const int64_t kv0 = load_index(a.kv_indptr, i64, seg);
-  const int64_t plen = load_index(a.kv_indptr, i64, seg + 1) - kv0;
-  const bool have_pos = a.q_pos != nullptr;
-  auto qpos_of = [&](int64_t i) -> int64_t {  // position of query i of the segment
-    return have_pos ? load_index(a.q_pos, a.pos_i64, qo0 + i) : plen + i;
+  const int32_t plen = static_cast<int32_t>(load_index(a.kv_indptr, i64, seg + 1) - kv0);
+  // segment-local views
+  const PosT* qpos = static_cast<const PosT*>(a.q_pos) + qo0;
+  const PosT* kpos = static_cast<const PosT*>(a.kv_pos) + kv0;
+  const IdxT* slots = static_cast<const IdxT*>(a.kv_indices) + kv0;
+  const __bf16* kext = a.k_ext + qo0 * a.ke_st + g * a.ke_sh;
+  const __bf16* vext = a.v_ext + qo0 * a.ve_st + g * a.ve_sh;
+  const __bf16* kpool = a.k_pool + g * a.kp_sh;
+  const __bf16* vpool = a.v_pool + g * a.vp_sh;
+  auto qpos_of = [&](int32_t i) -> int64_t {  // position of query i of the segment
+    if constexpr (POS) return static_cast<int64_t>(qpos[i]);
+    return static_cast<int64_t>(plen) + i;
   };
-  auto kpos_of = [&](int64_t j) -> int64_t {  // position of prefix key j
-    return have_pos ? load_index(a.kv_pos, a.pos_i64, kv0 + j) : j;
+  auto kpos_of = [&](int32_t j) -> int64_t {  // position of prefix key j
+    if constexpr (POS) return static_cast<int64_t>(kpos[j]);
+    return static_cast<int64_t>(j);
   };
+  const int64_t qbase = qpos_of(t0);
+  const int32_t e_hi = qlen < t0 + T ? qlen : t0 + T;  // extend keys [e_lo, e_hi)
+  const int32_t last_rel = rel_pos(qpos_of(e_hi - 1), qbase);
 
-  // key ranges: prefix [p_lo, plen), extend [e_lo, e_hi)
-  const int64_t e_hi = qlen < t0 + T ? qlen : t0 + T;
-  int64_t p_lo = 0, e_lo = 0;
+  // keys below qbase - window are outside every row's window
+  int32_t p_lo = 0, e_lo = 0;
   if (a.window >= 0) {
-    const int64_t first = qpos_of(t0) - a.window;  // keys below this position are out of every row's window
-    int64_t lo = 0, hi = plen;
+    const int64_t first = qbase - a.window;
+    int32_t lo = 0, hi = plen;
     while (lo < hi) {
-      const int64_t mid = (lo + hi) >> 1;
+      const int32_t mid = (lo + hi) >> 1;
       if (kpos_of(mid) < first) lo = mid + 1; else hi = mid;
     }
     p_lo = lo;
     lo = 0;
     hi = t0;
     while (lo < hi) {
-      const int64_t mid = (lo + hi) >> 1;
+      const int32_t mid = (lo + hi) >> 1;
       if (qpos_of(mid) < first) lo = mid + 1; else hi = mid;
     }
     e_lo = lo;
   }
-  const int n_pref = static_cast<int>((plen - p_lo + kKeys - 1) / kKeys);
-  const int n_tiles = n_pref + static_cast<int>((e_hi - e_lo + kKeys - 1) / kKeys);
+  const int n_pref = (plen - p_lo + kKeys - 1) / kKeys;
+  const int n_tiles = n_pref + (e_hi - e_lo + kKeys - 1) / kKeys;
+  auto tile_base = [&](int it) -> int32_t {
+    return it < n_pref ? p_lo + it * kKeys : e_lo + (it - n_pref) * kKeys;
+  };
 
   // this lane's rows: row subtile s covers rows wave*32 + 16s + col
-  int64_t row_tok[2], row_pos[2];
-  bool row_ok[2];
+  int32_t row_tl[2], row_rel[2];  // token within the block, position relative to qbase
   int row_head[2];
+  bool row_ok[2];
   bf16x8 qop[2][kKSteps];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const int r = wave * 32 + 16 * s + col;
     const int tl = r / G;
+    row_tl[s] = tl;
     row_head[s] = g * G + (r - tl * G);
-    row_tok[s] = t0 + tl;
-    row_ok[s] = tl < T && row_tok[s] < qlen;
-    row_pos[s] = row_ok[s] ? qpos_of(row_tok[s]) : 0;
+    row_ok[s] = t0 + tl < qlen;
+    row_rel[s] = row_ok[s] ? rel_pos(qpos_of(t0 + tl), qbase) : last_rel;
 #pragma unroll
     for (int ks = 0; ks < kKSteps; ++ks) {
       u32x4 w = {0u, 0u, 0u, 0u};
       if (row_ok[s])
-        w = load16(a.q + (qo0 + row_tok[s]) * a.q_st + row_head[s] * a.q_sh + 32 * ks + 8 * quad);
+        w = load16(a.q + (qo0 + t0 + tl) * a.q_st + static_cast<int64_t>(row_head[s]) * a.q_sh + 32 * ks + 8 * quad);
       qop[s][ks] = __builtin_bit_cast(bf16x8, w);
     }
   }
 
-  // tile staging: global -> registers -> LDS
-  u32x4 kreg[kKLoads];
-  u32x4 vreg[kVLoads][2];
-  int64_t preg = 0;
-  auto key_src = [&](int it, int key, bool& ok, const __bf16*& kr, const __bf16*& vr) {
-    if (it < n_pref) {
-      const int64_t j = p_lo + static_cast<int64_t>(it) * kKeys + key;
-      ok = j < plen;
-      if (ok) {
-        const int64_t slot = load_index(a.kv_indices, a.indices_i64, kv0 + j);
-        kr = a.k_pool + slot * a.kp_ss + g * a.kp_sh;
-        vr = a.v_pool + slot * a.vp_ss + g * a.vp_sh;
-      }
-    } else {
-      const int64_t j = e_lo + static_cast<int64_t>(it - n_pref) * kKeys + key;
-      ok = j < e_hi;
-      if (ok) {
-        kr = a.k_ext + (qo0 + j) * a.ke_st + g * a.ke_sh;
-        vr = a.v_ext + (qo0 + j) * a.ve_st + g * a.ve_sh;
+  // tile staging: thread item u = key pair p (keys 2p, 2p+1) x 16 B chunk cc,
+  // for K and V.  Prefix slots are fetched one tile ahead of their rows.
+  int64_t slot[kRounds][2];
+  u32x4 kreg[kRounds][2], vreg[kRounds][2];
+  int64_t preg = 0;  // raw position of key tid of the staged tile
+  bool pvalid = false;
+  auto fetch_slots = [&](int it) {
+    // keys past the prefix read the last prefix row (finite data, masked out)
+    const int32_t base = tile_base(it);
+#pragma unroll
+    for (int u = 0; u < kRounds; ++u) {
+      const int p = (tid + kThreads * u) / kChunks;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int32_t j = base + 2 * p + e;
+        slot[u][e] = static_cast<int64_t>(slots[j < plen ? j : plen - 1]);
       }
     }
   };
   auto stage = [&](int it) {
+    // branch-free: keys past the end read the last valid row (masked out later)
+    const bool ext = it >= n_pref;
+    const int32_t base = tile_base(it);
+    if (ext) {
 #pragma unroll
-    for (int u = 0; u < kKLoads; ++u) {
-      const int c = tid + kThreads * u;
-      const int key = c / kChunks;
-      const int cc = c - key * kChunks;
-      bool ok;
-      const __bf16 *kr = nullptr, *vr = nullptr;
-      key_src(it, key, ok, kr, vr);
-      kreg[u] = ok ? load16(kr + 8 * cc) : u32x4{0u, 0u, 0u, 0u};
-    }
+      for (int u = 0; u < kRounds; ++u) {
+        const int c = tid + kThreads * u;
+        const int p = c / kChunks;
+        const int cc = c - p * kChunks;
 #pragma unroll
-    for (int u = 0; u < kVLoads; ++u) {
-      const int c = tid + kThreads * u;
-      const int pair = c / kChunks;
-      const int cc = c - pair * kChunks;
+        for (int e = 0; e < 2; ++e) {
+          const int32_t j = base + 2 * p + e;
+          const int64_t off = static_cast<int64_t>(j < e_hi ? j : e_hi - 1);
+          kreg[u][e] = load16(kext + off * a.ke_st + 8 * cc);
+          vreg[u][e] = load16(vext + off * a.ve_st + 8 * cc);
+        }
+      }
+    } else {
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        bool ok;
-        const __bf16 *kr = nullptr, *vr = nullptr;
-        key_src(it, 2 * pair + e, ok, kr, vr);
-        vreg[u][e] = ok ? load16(vr + 8 * cc) : u32x4{0u, 0u, 0u, 0u};
+      for (int u = 0; u < kRounds; ++u) {
+        const int c = tid + kThreads * u;
+        const int p = c / kChunks;
+        const int cc = c - p * kChunks;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          kreg[u][e] = load16(kpool + slot[u][e] * a.kp_ss + 8 * cc);
+          vreg[u][e] = load16(vpool + slot[u][e] * a.vp_ss + 8 * cc);
+        }
       }
     }
     if (tid < kKeys) {
-      if (it < n_pref) {
-        const int64_t j = p_lo + static_cast<int64_t>(it) * kKeys + tid;
-        preg = j < plen ? kpos_of(j) : 0;
-      } else {
-        const int64_t j = e_lo + static_cast<int64_t>(it - n_pref) * kKeys + tid;
-        preg = j < e_hi ? qpos_of(j) : 0;
-      }
+      // loaded now, converted at commit: no wait on the tile's row loads here
+      const int32_t j = base + tid;
+      const int32_t end = ext ? e_hi : plen;
+      pvalid = j < end;
+      const int32_t jc = pvalid ? j : end - 1;
+      preg = ext ? qpos_of(jc) : kpos_of(jc);
     }
   };
   auto commit = [&](int buf) {
 #pragma unroll
-    for (int u = 0; u < kKLoads; ++u) {
+    for (int u = 0; u < kRounds; ++u) {
       const int c = tid + kThreads * u;
-      const int key = c / kChunks;
-      const int cc = c - key * kChunks;
-      *reinterpret_cast<u32x4*>(&sm.k[buf][key][8 * cc]) = kreg[u];
-    }
-#pragma unroll
-    for (int u = 0; u < kVLoads; ++u) {
-      const int c = tid + kThreads * u;
-      const int pair = c / kChunks;
-      const int cc = c - pair * kChunks;
-      // 8 dims x 2 keys -> 8 words of vt[dim][2 pair .. 2 pair + 1]
+      const int p = c / kChunks;
+      const int cc = c - p * kChunks;
+      *reinterpret_cast<u32x4*>(&sm.k[buf][2 * p][8 * cc]) = kreg[u][0];
+      *reinterpret_cast<u32x4*>(&sm.k[buf][2 * p + 1][8 * cc]) = kreg[u][1];
+      // 8 dims x 2 keys -> 8 words of vt[dim][2p .. 2p+1]
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const uint32_t lo = vreg[u][0][w];
         const uint32_t hi = vreg[u][1][w];
-        *reinterpret_cast<uint32_t*>(&sm.vt[buf][8 * cc + 2 * w][2 * pair]) = (lo & 0xffffu) | (hi << 16);
-        *reinterpret_cast<uint32_t*>(&sm.vt[buf][8 * cc + 2 * w + 1][2 * pair]) = (lo >> 16) | (hi & 0xffff0000u);
+        *reinterpret_cast<uint32_t*>(&sm.vt[buf][8 * cc + 2 * w][2 * p]) = (lo & 0xffffu) | (hi << 16);
+        *reinterpret_cast<uint32_t*>(&sm.vt[buf][8 * cc + 2 * w + 1][2 * p]) = (lo >> 16) | (hi & 0xffff0000u);
       }
     }
-    if (tid < kKeys) sm.pos[buf][tid] = preg;
+    if (tid < kKeys) sm.pos[buf][tid] = pvalid ? rel_pos(preg, qbase) : kFar;
   };
 
   f32x4 oacc[kDTiles][2];
@@ -249,16 +266,26 @@ __global__ void __launch_bounds__(kThreads) context_attention_kernel(const CtxAr
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_run[2] = {0.f, 0.f};
 
+  if (n_pref > 0) fetch_slots(0);
   stage(0);
+  if (1 < n_pref) fetch_slots(1);
   commit(0);
   __syncthreads();
   for (int it = 0; it < n_tiles; ++it) {
     const int buf = it & 1;
-    if (it + 1 < n_tiles) stage(it + 1);
+    if (it + 1 < n_tiles) {
+      stage(it + 1);
+      if (it + 2 < n_pref) fetch_slots(it + 2);
+    }
     const bool ext = it >= n_pref;
-    const int64_t base = ext ? e_lo + static_cast<int64_t>(it - n_pref) * kKeys
-                             : p_lo + static_cast<int64_t>(it) * kKeys;
-    const int64_t limit = ext ? e_hi : plen;
+    const int32_t base = tile_base(it);
+    const int32_t left = (ext ? e_hi : plen) - base;
+    const int count = left < kKeys ? left : kKeys;
+    // masking is needed for a partial tile, keys past the block's first
+    // query (causal), or keys older than the last query's window
+    const int32_t pos0 = __builtin_amdgcn_readfirstlane(sm.pos[buf][0]);
+    const bool masked = count < kKeys || (ext && base + kKeys - 1 > t0) ||
+                        (a.window >= 0 && pos0 < last_rel - a.window);
 
     // S^T = K . Q^T
     f32x4 sacc[4][2];
@@ -276,49 +303,70 @@ __global__ void __launch_bounds__(kThreads) context_attention_kernel(const CtxAr
       }
     }
 
-    // mask, online softmax (rows are columns of S^T: lanes col, col+16, col+32, col+48)
+    // online softmax per row (column of S^T: lanes col, col+16, col+32, col+48),
+    // log2 domain.  The reference maximum m_run moves only when a tile's
+    // maximum exceeds it by more than kLazy, so most tiles skip rescaling
+    // O and l; p = 2^(t - m_run) then stays below 2^kLazy.
     bf16x8 pop[2][2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      float sc[4][4];
+      float raw[4][4];
+      bool vis[4][4];
       float mx = -INFINITY;
+      if (masked) {
+        // causal: key index <= the row's token; window: key pos >= row pos - W
+        const int32_t climit = ext ? t0 + row_tl[s] - base : kKeys;
+        const int32_t last = climit < count - 1 ? climit : count - 1;
+        const int32_t thr = a.window >= 0 ? row_rel[s] - a.window : -kFar - 1;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = 16 * kt + 4 * quad + i;
-          const int64_t j = base + key;
-          bool vis = row_ok[s] && j < limit;
-          if (ext) vis = vis && j <= row_tok[s];
-          if (a.window >= 0) vis = vis && row_pos[s] <= sm.pos[buf][key] + a.window;
-          sc[kt][i] = vis ? sacc[kt][s][i] * a.scale_log2 : -INFINITY;
-          mx = fmaxf(mx, sc[kt][i]);
-        }
+          for (int i = 0; i < 4; ++i) {
+            const int key = 16 * kt + 4 * quad + i;
+            vis[kt][i] = key <= last && sm.pos[buf][key] >= thr;
+            raw[kt][i] = sacc[kt][s][i];
+            if (vis[kt][i]) mx = fmaxf(mx, raw[kt][i]);
+          }
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            vis[kt][i] = true;
+            raw[kt][i] = sacc[kt][s][i];
+            mx = fmaxf(mx, raw[kt][i]);
+          }
+      }
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[s], mx);
-      const bool live = m_new != -INFINITY;
-      const float alpha = live ? exp2f(m_run[s] - m_new) : 1.f;
-      float psum = 0.f;
+      const float tmax = mx * a.scale_log2;  // -inf when the row sees nothing here
+      const bool bump = tmax > m_run[s] + kLazy;
+      if (__builtin_amdgcn_ballot_w64(bump)) {
+        const float m_new = bump ? tmax : m_run[s];
+        const float alpha = bump ? __builtin_amdgcn_exp2f(m_run[s] - m_new) : 1.f;  // m_run = -inf -> 0
+        l_run[s] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] *= alpha;
+        m_run[s] = m_new;
+      }
+      const float neg_m = -m_run[s];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = live ? exp2f(sc[kt][i] - m_new) : 0.f;
-          sc[kt][i] = p;
-          psum += p;
-        }
-      l_run[s] = l_run[s] * alpha + psum;
-      m_run[s] = m_new;
-#pragma unroll
-      for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] *= alpha;
+        for (int i = 0; i < 4; ++i)
+          raw[kt][i] = vis[kt][i] ? __builtin_amdgcn_exp2f(fmaf(raw[kt][i], a.scale_log2, neg_m)) : 0.f;
+      // the denominator sums the same bf16-rounded weights the PV product
+      // uses, so the output stays a convex combination of the values
+      float psum = 0.f;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          pop[s][kk][i] = static_cast<__bf16>(sc[2 * kk][i]);
-          pop[s][kk][4 + i] = static_cast<__bf16>(sc[2 * kk + 1][i]);
+          pop[s][kk][i] = static_cast<__bf16>(raw[2 * kk][i]);
+          pop[s][kk][4 + i] = static_cast<__bf16>(raw[2 * kk + 1][i]);
+          psum += static_cast<float>(pop[s][kk][i]) + static_cast<float>(pop[s][kk][4 + i]);
         }
+      l_run[s] += psum;
     }
 
     // O^T += V^T . P^T
@@ -354,7 +402,8 @@ __global__ void __launch_bounds__(kThreads) context_attention_kernel(const CtxAr
     }
     const float inv = l > 0.f ? scale / l : 0.f;
     if (!row_ok[s]) continue;
-    const int64_t at = (qo0 + row_tok[s]) * a.o_st + row_head[s] * a.o_sh + 4 * quad;
+    const int64_t at =
+        (qo0 + t0 + row_tl[s]) * a.o_st + static_cast<int64_t>(row_head[s]) * a.o_sh + 4 * quad;
 #pragma unroll
     for (int dt = 0; dt < kDTiles; ++dt) {
       const f32x4 o = oacc[dt][s] * inv;
@@ -368,6 +417,32 @@ __global__ void __launch_bounds__(kThreads) context_attention_kernel(const CtxAr
       }
     }
   }
+}
+
+template <int D, typename IdxT>
+void launch_pos(int pos, dim3 grid, hipStream_t st, const CtxArgs& a) {
+  // pos: 0 none, 1 int32, 2 int64
+  if (pos == 2)
+    hipLaunchKernelGGL((context_attention_kernel<D, IdxT, int64_t, true>), grid, dim3(kThreads), 0, st, a);
+  else if (pos == 1)
+    hipLaunchKernelGGL((context_attention_kernel<D, IdxT, int32_t, true>), grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((context_attention_kernel<D, IdxT, int64_t, false>), grid, dim3(kThreads), 0, st, a);
+}
+
+template <int D>
+void launch_idx(bool idx64, int pos, dim3 grid, hipStream_t st, const CtxArgs& a) {
+  if (idx64)
+    launch_pos<D, int64_t>(pos, grid, st, a);
+  else
+    launch_pos<D, int32_t>(pos, grid, st, a);
+}
+
+void launch_typed(int head_dim, bool idx64, int pos, dim3 grid, hipStream_t st, const CtxArgs& a) {
+  if (head_dim == 64)
+    launch_idx<64>(idx64, pos, grid, st, a);
+  else
+    launch_idx<128>(idx64, pos, grid, st, a);
 }
 
 }  // namespace
@@ -404,8 +479,10 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
   const int64_t strides[] = {q_stride_t,    q_stride_h,    k_ext_stride_t, k_ext_stride_h, v_ext_stride_t,
                              v_ext_stride_h, k_stride_slot, k_stride_head,  v_stride_slot,  v_stride_head,
                              out_stride_t,  out_stride_h};
-  for (int64_t s : strides)
+  for (int64_t s : strides) {
     if (s % 8 != 0) return fail(AKV_EINVAL, "akv_context_attention: row strides must be multiples of 8 elements");
+    if (s < 0 || s > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_context_attention: strides must fit 31 bits");
+  }
   const uintptr_t bases = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_ext) |
                           reinterpret_cast<uintptr_t>(v_ext) | reinterpret_cast<uintptr_t>(k_buffer) |
                           reinterpret_cast<uintptr_t>(v_buffer) | reinterpret_cast<uintptr_t>(out);
@@ -414,45 +491,41 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
     return fail(AKV_EINVAL, "akv_context_attention: batch too large");
   CtxArgs a{};
   a.q = static_cast<const __bf16*>(q);
-  a.q_st = q_stride_t;
-  a.q_sh = q_stride_h;
   a.k_ext = static_cast<const __bf16*>(k_ext);
   a.v_ext = static_cast<const __bf16*>(v_ext);
-  a.ke_st = k_ext_stride_t;
-  a.ke_sh = k_ext_stride_h;
-  a.ve_st = v_ext_stride_t;
-  a.ve_sh = v_ext_stride_h;
   a.k_pool = static_cast<const __bf16*>(k_buffer);
   a.v_pool = static_cast<const __bf16*>(v_buffer);
-  a.kp_ss = k_stride_slot;
-  a.kp_sh = k_stride_head;
-  a.vp_ss = v_stride_slot;
-  a.vp_sh = v_stride_head;
   a.qo_indptr = qo_indptr;
   a.kv_indptr = kv_indptr;
   a.kv_indices = kv_indices;
   a.q_pos = q_positions;
   a.kv_pos = kv_positions;
-  a.indptr_i64 = indptr_dtype == AKV_I64;
-  a.indices_i64 = indices_dtype == AKV_I64;
-  a.pos_i64 = positions_dtype == AKV_I64;
-  a.window = sliding_window < 0 ? -1 : sliding_window;
   a.sinks = sinks;
-  a.scale_log2 = scale * kLog2e;
   a.out = out;
+  a.q_st = static_cast<int32_t>(q_stride_t);
+  a.q_sh = static_cast<int32_t>(q_stride_h);
+  a.ke_st = static_cast<int32_t>(k_ext_stride_t);
+  a.ke_sh = static_cast<int32_t>(k_ext_stride_h);
+  a.ve_st = static_cast<int32_t>(v_ext_stride_t);
+  a.ve_sh = static_cast<int32_t>(v_ext_stride_h);
+  a.kp_ss = static_cast<int32_t>(k_stride_slot);
+  a.kp_sh = static_cast<int32_t>(k_stride_head);
+  a.vp_ss = static_cast<int32_t>(v_stride_slot);
+  a.vp_sh = static_cast<int32_t>(v_stride_head);
+  a.o_st = static_cast<int32_t>(out_stride_t);
+  a.o_sh = static_cast<int32_t>(out_stride_h);
+  a.indptr_i64 = indptr_dtype == AKV_I64;
+  a.window = sliding_window < 0 ? -1 : sliding_window;
+  a.scale_log2 = scale * kLog2e;
   a.out_f32 = out_dtype == AKV_F32;
-  a.o_st = out_stride_t;
-  a.o_sh = out_stride_h;
-  a.kv_heads = kv_heads;
   a.group = q_heads / kv_heads;
   a.tokens_per_block = kRows / a.group;
   const int64_t blocks = (max_query_len + a.tokens_per_block - 1) / a.tokens_per_block;
   if (blocks > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_context_attention: queries too long");
   const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(kv_heads), static_cast<unsigned>(n_segments));
   hipStream_t st = as_stream(stream);
-  if (head_dim == 64)
-    hipLaunchKernelGGL(context_attention_kernel<64>, grid, dim3(kThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL(context_attention_kernel<128>, grid, dim3(kThreads), 0, st, a);
+  const bool idx64 = indices_dtype == AKV_I64;
+  const int pos = q_positions == nullptr ? 0 : (positions_dtype == AKV_I64 ? 2 : 1);
+  launch_typed(head_dim, idx64, pos, grid, st, a);
   return check_launch("akv_context_attention");
 }

@@ -375,6 +375,57 @@ def cow_config(device, flush):
     }
 
 
+def prefill_config(device, flush, extend=4096):
+    """Next turn's prefill over the compacted 32k GPT-OSS request: 4096 new
+    tokens attend to the 19441 kept tokens (positions with the dropped holes)
+    and causally to themselves; a full layer and a 128-window layer (64 q /
+    8 KV heads x 64, sinks)."""
+    from akv_amd import context_attention as ca
+
+    w = synth.workload("gpt-oss-32k")
+    lay = synth.compile_layouts(w)[0]
+    keep = np.asarray(lay.keep_mask)
+    kept_pos = np.asarray(lay.positions)[keep].astype(np.int64)
+    plen = len(kept_pos)
+    nxt = int(lay.next_position)
+    qpos = np.arange(nxt, nxt + extend, dtype=np.int64)
+    hq, hkv, d = 64, 8, 64
+    slots = 2 * plen + 1
+    g = torch.Generator(device=device)
+    g.manual_seed(11)
+    q = torch.randn((extend, hq, d), generator=g, device=device).to(torch.bfloat16)
+    ke = torch.randn((extend, hkv, d), generator=g, device=device).to(torch.bfloat16)
+    ve = torch.randn((extend, hkv, d), generator=g, device=device).to(torch.bfloat16)
+    kp = torch.randn((slots, hkv, d), generator=g, device=device).to(torch.bfloat16)
+    vp = torch.randn((slots, hkv, d), generator=g, device=device).to(torch.bfloat16)
+    sinks = torch.randn(hq, generator=g, device=device)
+    rng = np.random.default_rng(11)
+    idx = torch.from_numpy(rng.permutation(np.arange(1, slots))[:plen].astype(np.int32)).to(device)
+    qo = torch.tensor([0, extend], dtype=torch.int64, device=device)
+    kv = torch.tensor([0, plen], dtype=torch.int64, device=device)
+    qp = torch.from_numpy(qpos).to(device)
+    kpp = torch.from_numpy(kept_pos).to(device)
+    out = torch.empty_like(q)
+
+    def layer(window):
+        return lambda: ca.extend_attention_fwd(q, ke, ve, out, kp, vp, qo, kv, idx, None, True, None, extend,
+                                               sm_scale=0.125, sliding_window_size=window, sinks=sinks,
+                                               context_q_positions=qp, context_kv_positions=kpp)
+
+    warm_full, cold_full = _time_steps(layer(-1), 10, 3, 10, flush)
+    warm_win, cold_win = _time_steps(layer(128), 20, 3, 10, flush)
+    # causal flops: QK^T and PV, 2 flops per multiply-add each
+    flops_full = 4 * hq * d * sum(plen + i + 1 for i in range(extend))
+    return {
+        "workload": f"gpt-oss-120b prefill of {extend} tokens over {plen} kept tokens (64 q / 8 KV heads x 64, sinks)",
+        "full_layer_ms": round(warm_full, 4), "full_layer_p50_ms": round(percentile(cold_full, 50), 4),
+        "full_layer_TFLOPs": round(flops_full / (warm_full / 1e3) / 1e12, 1),
+        "full_layer_pct_mfma_bf16_peak": round(100 * flops_full / (warm_full / 1e3) / 2.5e15, 2),
+        "window128_layer_ms": round(warm_win, 4), "window128_layer_p50_ms": round(percentile(cold_win, 50), 4),
+        "kernel_launches_per_layer": 1,
+    }
+
+
 def read_pmc_traffic():
     """HBM bytes per Reposition launch from the committed rocprof PMC summary."""
     if not PMC_SUMMARY.exists():
@@ -579,7 +630,8 @@ def main():
     if not args.reposition_only:
         print("# secondary configurations ...", file=sys.stderr, flush=True)
         result["other_configs"] = [tiny_config(device, pipe.flush), ascending_slots_config(device, pipe.flush),
-                                   ragged_config(device, pipe.flush), decode_consumer_config(device, pipe.flush)]
+                                   ragged_config(device, pipe.flush), decode_consumer_config(device, pipe.flush),
+                                   prefill_config(device, pipe.flush)]
         if not args.no_cow:
             print("# copy-on-write configuration ...", file=sys.stderr, flush=True)
             result["other_configs"].append(cow_config(device, pipe.flush))
