@@ -90,7 +90,7 @@ __device__ __forceinline__ int32_t rel_pos(int64_t p, int64_t base) {
 }
 
 template <int D, typename IdxT, typename PosT, bool POS>
-__global__ void __launch_bounds__(kThreads) context_attention_kernel(const CtxArgs a) {
+__global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_kernel(const CtxArgs a) {
   constexpr int kChunks = D / 8;               // 16 B chunks per key row
   constexpr int kRounds = kChunks / 8;         // (key pair, chunk) items per thread
   constexpr int kKSteps = D / 32;              // MFMA k-steps over head dims
@@ -264,7 +264,9 @@ __global__ void __launch_bounds__(kThreads) context_attention_kernel(const CtxAr
 #pragma unroll
     for (int s = 0; s < 2; ++s) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.f, 0.f};
+  f32x4 lacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};  // row sums (4 equal copies)
+  const bf16x8 kOnes = {__bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f),
+                        __bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f)};
 
   if (n_pref > 0) fetch_slots(0);
   stage(0);
@@ -344,7 +346,7 @@ __global__ void __launch_bounds__(kThreads) context_attention_kernel(const CtxAr
       if (__builtin_amdgcn_ballot_w64(bump)) {
         const float m_new = bump ? tmax : m_run[s];
         const float alpha = bump ? __builtin_amdgcn_exp2f(m_run[s] - m_new) : 1.f;  // m_run = -inf -> 0
-        l_run[s] *= alpha;
+        lacc[s] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] *= alpha;
         m_run[s] = m_new;
@@ -355,18 +357,13 @@ __global__ void __launch_bounds__(kThreads) context_attention_kernel(const CtxAr
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           raw[kt][i] = vis[kt][i] ? __builtin_amdgcn_exp2f(fmaf(raw[kt][i], a.scale_log2, neg_m)) : 0.f;
-      // the denominator sums the same bf16-rounded weights the PV product
-      // uses, so the output stays a convex combination of the values
-      float psum = 0.f;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           pop[s][kk][i] = static_cast<__bf16>(raw[2 * kk][i]);
           pop[s][kk][4 + i] = static_cast<__bf16>(raw[2 * kk + 1][i]);
-          psum += static_cast<float>(pop[s][kk][i]) + static_cast<float>(pop[s][kk][4 + i]);
         }
-      l_run[s] += psum;
     }
 
     // O^T += V^T . P^T
@@ -382,17 +379,22 @@ __global__ void __launch_bounds__(kThreads) context_attention_kernel(const CtxAr
         for (int s = 0; s < 2; ++s)
           oacc[dt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[s][kk], oacc[dt][s], 0, 0, 0);
       }
+    // row sums of the same bf16 weights on the matrix cores (a ones operand):
+    // the output stays a convex combination of the values
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        lacc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kOnes, pop[s][kk], lacc[s], 0, 0, 0);
 
     if (it + 1 < n_tiles) commit(buf ^ 1);
     __syncthreads();
   }
 
-  // normalise (row sums over the 4 lanes of a column) with the sink; store
+  // normalise with the sink; store
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    float l = l_run[s];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    float l = lacc[s][0];
     float scale = 1.f;
     if (a.sinks) {
       const float sink = a.sinks[row_head[s]] * kLog2e;
