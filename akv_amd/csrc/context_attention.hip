@@ -42,6 +42,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(1))) u32x4 global_u32x4;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr int kRows = 128;  // (token, head) rows per workgroup
 constexpr int kThreads = 256;
@@ -78,7 +80,7 @@ __device__ __forceinline__ u32x4 load16(const __bf16* p) {
 template <int D>
 struct Smem {
   __bf16 k[2][kKeys][D + 8];   // key-major K tile, rows padded by 16 B
-  __bf16 vt[2][D][kKeys + 4];  // dim-major V tile, rows padded by 8 B
+  __bf16 v[2][kKeys][D + 8];   // key-major V tile, read transposed (ds_read_b64_tr_b16)
   int32_t pos[2][kKeys];       // key positions relative to the block's first query
 };
 
@@ -246,14 +248,8 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
       const int cc = c - p * kChunks;
       *reinterpret_cast<u32x4*>(&sm.k[buf][2 * p][8 * cc]) = kreg[u][0];
       *reinterpret_cast<u32x4*>(&sm.k[buf][2 * p + 1][8 * cc]) = kreg[u][1];
-      // 8 dims x 2 keys -> 8 words of vt[dim][2p .. 2p+1]
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t lo = vreg[u][0][w];
-        const uint32_t hi = vreg[u][1][w];
-        *reinterpret_cast<uint32_t*>(&sm.vt[buf][8 * cc + 2 * w][2 * p]) = (lo & 0xffffu) | (hi << 16);
-        *reinterpret_cast<uint32_t*>(&sm.vt[buf][8 * cc + 2 * w + 1][2 * p]) = (lo >> 16) | (hi & 0xffff0000u);
-      }
+      *reinterpret_cast<u32x4*>(&sm.v[buf][2 * p][8 * cc]) = vreg[u][0];
+      *reinterpret_cast<u32x4*>(&sm.v[buf][2 * p + 1][8 * cc]) = vreg[u][1];
     }
     if (tid < kKeys) sm.pos[buf][tid] = pvalid ? rel_pos(preg, qbase) : kFar;
   };
@@ -371,10 +367,14 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
     for (int dt = 0; dt < kDTiles; ++dt)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(&sm.vt[buf][16 * dt + col][32 * kk + 4 * quad]);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(&sm.vt[buf][16 * dt + col][32 * kk + 16 + 4 * quad]);
-        const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
-        const bf16x8 vop = __builtin_bit_cast(bf16x8, w);
+        // transposing read: lane col of group quad receives V[key][16dt + col]
+        // for keys 32kk + 4 quad + i (i < 4), then 32kk + 16 + 4 quad + i;
+        // source lane col supplies row key0 + col / 4, dims 16dt + 4 (col % 4) ..+3
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)&sm.v[buf][32 * kk + 4 * quad + (col >> 2)][16 * dt + 4 * (col & 3)]);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)&sm.v[buf][32 * kk + 16 + 4 * quad + (col >> 2)][16 * dt + 4 * (col & 3)]);
+        const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int s = 0; s < 2; ++s)
           oacc[dt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[s][kk], oacc[dt][s], 0, 0, 0);
