@@ -18,17 +18,24 @@
 //
 // Workgroup = (block of 128 / G query tokens, KV head g, segment), with the
 // G q heads of the group packed as rows: row r = token * G + head, 128 rows,
-// 4 waves x 32 rows.  Per 64-key tile (K and V^T staged in LDS, double
-// buffered, the next tile's global loads in flight during this tile's math):
+// 4 waves x 32 rows.  Per 64-key tile (K and V key-major in LDS, double
+// buffered, the next tile's global loads -- and the slots of the tile after
+// it -- in flight during this tile's math):
 //   S^T[64 keys x 32 rows] = K . Q^T          v_mfma_f32_16x16x32_bf16
-//   online softmax per row (column of S^T) in the exp2 domain
+//   online softmax per row (column of S^T) in the exp2 domain, the running
+//   maximum moving only when a tile exceeds it by 2^8 (lazy rescale)
 //   O^T[D x 32 rows] += V^T . P^T             v_mfma_f32_16x16x32_bf16
+//   l[rows] += 1^T . P^T                      (row sums of the same bf16 P)
 // P^T leaves the first MFMA in the B-operand layout of the second (any
 // consistent split of the 32-long k axis over lanes gives the same product:
-// lane l uses keys 4(l/16)+i of two 16-key subtiles).
+// lane l uses keys 4(l/16)+i of two 16-key subtiles); V^T comes from the
+// key-major tile through ds_read_b64_tr_b16.  Tiles wholly inside every
+// row's causal and window range skip the mask.
 //
-// MFMA 16x16x32 bf16 lane layout (verified on gfx950): lane l supplies
-// A[l%16][k(l,i)], B[k(l,i)][l%16] for i < 8 and holds D[4(l/16)+i][l%16].
+// Lane layouts (verified on gfx950): v_mfma_f32_16x16x32_bf16 -- lane l
+// supplies A[l%16][k(l,i)], B[k(l,i)][l%16] for i < 8 and holds
+// D[4(l/16)+i][l%16]; ds_read_b64_tr_b16 -- within each 16-lane group, lane
+// j receives element j%4 of the 8-byte rows read by lanes j/4 + 4i, i < 4.
 #include <cmath>
 
 #include "common.h"
