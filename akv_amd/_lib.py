@@ -15,6 +15,7 @@ LIBRARY_PATH = Path(__file__).resolve().parent / "libakv_amd.so"
 AKV_OK = 0
 AKV_EINVAL = -22
 AKV_EHIP = -5
+AKV_ERUNTIME = -71
 AKV_F32, AKV_F16, AKV_BF16 = 0, 1, 2
 AKV_I32, AKV_I64 = 0, 1
 
@@ -67,6 +68,21 @@ _SIGNATURES = {
         [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64,
          c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, _P, _P, c_int32, _P, c_int32, _P, _P,
          c_int32, c_int32, _P, ctypes.c_float, _P, c_int32, c_int64, c_int64, c_int64, _P],
+    ),
+    "akv_bind_workspace_bytes": (c_int64, [c_int32, c_int64]),
+    "akv_bind_occurrences": (
+        c_int32,
+        [c_int32, _P, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, _P, _P,
+         c_int64, _P],
+    ),
+    "akv_window_count": (
+        c_int32,
+        [c_int64, _P, _P, _P, c_int64, _P, _P, _P, _P, _P, c_int64, c_int64, _P],
+    ),
+    "akv_window_compile": (
+        c_int32,
+        [c_int64, _P, _P, _P, c_int64, _P, _P, _P, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
+         _P, _P],
     ),
     "akv_plan_count": (
         c_int32,

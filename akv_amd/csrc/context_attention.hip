@@ -473,7 +473,7 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
   if (n_segments == 0 || max_query_len == 0) return AKV_OK;
   if (head_dim != 64 && head_dim != 128)
     return fail(AKV_EINVAL, "akv_context_attention: head_dim %d (supported: 64, 128)", head_dim);
-  if (kv_heads <= 0 || q_heads % kv_heads != 0 || kRows % (q_heads / kv_heads) != 0)
+  if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0 || kRows % (q_heads / kv_heads) != 0)
     return fail(AKV_EINVAL, "akv_context_attention: %d q heads over %d KV heads (group must divide %d)",
                 q_heads, kv_heads, kRows);
   if (!valid_index_dtype(indptr_dtype) || !valid_index_dtype(indices_dtype) ||

@@ -303,7 +303,7 @@ extern "C" int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q
   if (n_requests == 0) return AKV_OK;
   if (head_dim != 64 && head_dim != 128)
     return fail(AKV_EINVAL, "akv_decode_attention: head_dim %d (supported: 64, 128)", head_dim);
-  if (kv_heads <= 0 || q_heads % kv_heads != 0 || q_heads / kv_heads > 16)
+  if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0 || q_heads / kv_heads > 16)
     return fail(AKV_EINVAL, "akv_decode_attention: %d q heads over %d KV heads (group <= 16)", q_heads,
                 kv_heads);
   if (out_dtype != AKV_BF16 && out_dtype != AKV_F32)

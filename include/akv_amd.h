@@ -9,7 +9,8 @@
  * finished with them (the caller's lifetime contract).
  *
  * Return value: 0 on success, AKV_EINVAL for an invalid argument, AKV_EHIP
- * when the HIP runtime rejected a launch.  akv_last_error() returns the
+ * when the HIP runtime rejected a launch, AKV_ERUNTIME for an internal
+ * consistency failure the reference reports as RuntimeError.  akv_last_error() returns the
  * message of the last failure on the calling thread.
  *
  * Paths in the citations are relative to the reference repository root.
@@ -26,6 +27,7 @@ extern "C" {
 #define AKV_OK 0
 #define AKV_EINVAL (-22)
 #define AKV_EHIP (-5)
+#define AKV_ERUNTIME (-71)
 
 /* Storage dtypes of KV buffers and RoPE tables. */
 #define AKV_F32 0
@@ -273,6 +275,89 @@ int akv_context_attention(const void* q, int64_t q_stride_t,
                           float scale, void* out, int32_t out_dtype,
                           int64_t out_stride_t, int64_t out_stride_h,
                           int64_t max_query_len, void* stream);
+
+/*
+ * Host (CPU) occurrence window of one forward: the (raw token, position)
+ * versions its attention reads and the order in which they are first
+ * needed.  Inputs are the compiled layout's int32 vectors (birth positions
+ * and stages [n], transition offsets [stage_count+1] and raw / old / new
+ * [offsets[stage_count]]), visible_until [n] (a token is readable by
+ * queries before it) and terminal_positions [n].
+ * akv_window_count writes counts[4] = {occurrences, segments, keys,
+ * first_final}: occurrences [n, first_final) are versions read by a
+ * segment, [first_final, occurrences) the terminal versions materialised
+ * after the last stage.  akv_window_compile fills, for those counts:
+ * occurrence_raw_tokens / occurrence_positions [occurrences] (ids 0..n-1
+ * are the births), terminal_occurrences [n], segment_query_starts / ends
+ * [segments], segment_key_offsets [segments+1], segment_key_occurrences
+ * [keys].  Same results and messages as compile_occurrence_window,
+ * akv/system/sglang/srt/context_system/occurrence.py:112-265.
+ */
+int akv_window_count(int64_t n, const int32_t* birth_positions,
+                     const int32_t* birth_stages,
+                     const int32_t* transition_offsets, int64_t stage_count,
+                     const int32_t* transition_raw_tokens,
+                     const int32_t* transition_old_positions,
+                     const int32_t* transition_new_positions,
+                     const int32_t* visible_until,
+                     const int32_t* terminal_positions, int64_t query_start,
+                     int64_t query_end, int64_t* counts);
+
+int akv_window_compile(int64_t n, const int32_t* birth_positions,
+                       const int32_t* birth_stages,
+                       const int32_t* transition_offsets, int64_t stage_count,
+                       const int32_t* transition_raw_tokens,
+                       const int32_t* transition_old_positions,
+                       const int32_t* transition_new_positions,
+                       const int32_t* visible_until,
+                       const int32_t* terminal_positions, int64_t query_start,
+                       int64_t query_end, const int64_t* counts,
+                       int32_t* occurrence_raw_tokens,
+                       int32_t* occurrence_positions,
+                       int32_t* terminal_occurrences,
+                       int32_t* segment_query_starts,
+                       int32_t* segment_query_ends,
+                       int32_t* segment_key_offsets,
+                       int32_t* segment_key_occurrences);
+
+/*
+ * Device bytes of the scratch buffer akv_bind_occurrences needs.
+ */
+int64_t akv_bind_workspace_bytes(int32_t n_requests, int64_t max_occurrences);
+
+/*
+ * Slot binding of a fresh request's whole-prompt forward (query_start = 0,
+ * query_end = n, every slot request-owned) from its occurrence window
+ * (akv_window_compile): for request b, occurrences bases[0][b] ..
+ * bases[0][b+1] (request-local raw index and position; ids < n are the
+ * births), raw tokens bases[1][b] .. bases[1][b+1] (terminal occurrence,
+ * keep, birth slot).  A version is required when it is a birth, read by a
+ * segment (id < first_final = bases[5][b]) or the terminal version of a
+ * kept token; it reuses the birth slot when its position is the birth
+ * position, else it takes the next fresh slot (occurrence order) and a copy
+ * (birth slot -> fresh slot, (birth position, position)).
+ * Outputs: occurrence_slots (-1 for versions nothing needs), copy lists at
+ * bases[2][b] .., retired at bases[3][b] .. (birth slots that are not
+ * terminal, raw order; then, from bases[4][b], fresh slots that are not
+ * terminal, allocation order), and the request row (table row req_rows[b]
+ * or row_pointers[req_rows[b]]): kept ? terminal slot : -1.
+ * bases int64 [6, B+1] are host-computed; every write is bounded by them.
+ * Replaces plan_occurrence_materialization + OccurrenceState.advance +
+ * terminal_slots for that forward,
+ * akv/system/sglang/srt/context_system/occurrence.py:341-466,632-767.
+ */
+int akv_bind_occurrences(int32_t n_requests, const int64_t* bases,
+                         int64_t max_occurrences,
+                         const int32_t* occurrence_raw_tokens,
+                         const int32_t* occurrence_positions,
+                         const int32_t* terminal_occurrences,
+                         const uint8_t* keep, const int32_t* birth_slots,
+                         const int32_t* fresh_slots, int32_t* occurrence_slots,
+                         int32_t* copy_src, int32_t* copy_dst,
+                         int32_t* copy_pairs, int32_t* retired, int32_t* table,
+                         int64_t row_stride, const int64_t* row_pointers,
+                         const int64_t* req_rows, void* workspace,
+                         int64_t workspace_bytes, void* stream);
 
 /*
  * Host event compiler (CPU, no device work).  Replays Drop and Reposition

@@ -55,6 +55,15 @@ def test_validation_rejects_before_any_device_work(lib):
     assert "page_size" in _lib.last_error()
     assert lib.akv_compact_pages(*zeros(lib.akv_compact_pages, a0=2, a2=5, a3=16)) == _lib.AKV_EINVAL
     assert "null device pointer" in _lib.last_error()
+    assert lib.akv_bind_occurrences(*zeros(lib.akv_bind_occurrences, a0=-1)) == _lib.AKV_EINVAL
+    assert lib.akv_bind_occurrences(*zeros(lib.akv_bind_occurrences)) == 0  # empty batch
+    assert lib.akv_bind_occurrences(*zeros(lib.akv_bind_occurrences, a0=2, a2=9)) == _lib.AKV_EINVAL
+    assert "null device pointer" in _lib.last_error()
+    assert lib.akv_bind_workspace_bytes(4, 100000) > 0
+    assert lib.akv_context_attention(*zeros(lib.akv_context_attention, a15=1, a17=1, a18=64, a34=4)) == _lib.AKV_EINVAL
+    assert lib.akv_window_count(*zeros(lib.akv_window_count)) == _lib.AKV_EINVAL
+    assert lib.akv_decode_attention(*zeros(lib.akv_decode_attention, a9=1, a11=1, a12=64)) == _lib.AKV_EINVAL
+    assert "q heads" in _lib.last_error()
     ws = lib.akv_compact_workspace_bytes(64, 65536)
     assert ws > 0
     assert lib.akv_decode_indices(*zeros(lib.akv_decode_indices)) == 0
