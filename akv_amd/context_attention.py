@@ -138,8 +138,9 @@ class ContextAttentionPlan:
             or occurrence_slots.dtype not in (torch.int32, torch.int64)
         ):
             raise ValueError("Physical slot binding must cover all batch occurrences")
-        host = self.packed.pin_memory() if torch.cuda.is_available() else self.packed
-        packed = host.to(device=occurrence_slots.device, non_blocking=True)
+        # one staged copy from pageable memory (a fresh pinned buffer per call
+        # costs more than the copy of this size)
+        packed = self.packed.to(device=occurrence_slots.device, non_blocking=True)
         qo, kv, occurrences, q_positions, kv_positions = [packed[a:b] for a, b in self.field_ranges]
         return ContextAttentionMetadata(
             qo,

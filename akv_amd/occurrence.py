@@ -184,10 +184,9 @@ def pack_final_forward(windows, keep_masks, device):
     packed[at2 : at2 + total_n] = np.concatenate([w.terminal_occurrences.numpy() for w in windows])
     at3 = at2 + total_n
     packed[at3:].view(np.uint8)[:total_n] = np.concatenate([np.asarray(k, dtype=np.uint8) for k in keep_masks])
-    host = torch.from_numpy(packed)
-    if torch.cuda.is_available():
-        host = host.pin_memory()
-    dev = host.to(device, non_blocking=True)
+    # one staged copy from pageable memory (a fresh pinned buffer per call
+    # costs more than the copy of this size)
+    dev = torch.from_numpy(packed).to(device, non_blocking=True)
     return FinalForwardInputs(
         bases=dev[: 2 * bases.size].view(torch.int64).view(6, B + 1),
         occurrence_raw_tokens=dev[at : at + total_occ],

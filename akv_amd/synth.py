@@ -266,6 +266,40 @@ def workload(name):
     raise ValueError(f"unknown workload {name!r}")
 
 
+def trajectory_events(n, turns, lo, hi, seed):
+    """A multi-turn agent prompt compiled in one prefill: at each of ``turns-1``
+    turn boundaries (evenly spaced insertion points) 1-2 tool-output spans of
+    ``U[lo, hi]`` tokens inside the previous turn are dropped and the context
+    is repositioned.  Returns the event tensors and ``visible_until`` (a
+    dropped token is readable by the queries before its drop)."""
+    rng = np.random.default_rng(seed)
+    bounds = [n * t // turns for t in range(1, turns)]
+    inserts, offsets, flat = [], [0], []
+    visible = np.full(n, np.iinfo(np.int32).max, dtype=np.int64)
+    prev = 0
+    for at in bounds:
+        k = int(rng.integers(1, 3))
+        lengths = rng.integers(lo, hi + 1, size=k)
+        if int(lengths.sum()) + k >= at - prev:
+            lengths = np.maximum(1, lengths * (at - prev - k - 1) // (int(lengths.sum()) + 1))
+        spans = place_spans(rng, at - prev, lengths)
+        for s, e in spans:
+            flat += [prev + s, prev + e]
+            visible[prev + s : prev + e] = at
+        inserts.append(at)
+        offsets.append(len(flat) // 2)
+        prev = at
+    events = dict(
+        token_ids=torch.arange(n, dtype=torch.int32) % 50000,
+        drop_insert_offsets=torch.tensor(inserts, dtype=torch.int32),
+        drop_range_offsets=torch.tensor(offsets, dtype=torch.int32),
+        drop_ranges=torch.tensor(flat, dtype=torch.int32),
+        reposition_raw_boundaries=torch.tensor(inserts, dtype=torch.int32) - 1,
+        reposition_insert_offsets=torch.tensor(inserts, dtype=torch.int32),
+    )
+    return events, torch.from_numpy(visible.astype(np.int32))
+
+
 def request_events(n, spans):
     """Event tensors of one Drop (all spans) + one Reposition, both at insertion n."""
     flat = [x for span in spans for x in span]

@@ -87,8 +87,9 @@ def pack_compaction_inputs(layouts, device):
     keep_bytes = packed[2 * total + 2 * len(offsets) :].view(np.uint8)
     if total:
         keep_bytes[:total] = np.concatenate(keeps).astype(np.uint8)
-    host = torch.from_numpy(packed).pin_memory() if torch.cuda.is_available() else torch.from_numpy(packed)
-    dev = host.to(device, non_blocking=True)
+    # one staged copy from pageable memory (a fresh pinned buffer per call
+    # costs more than the copy of this size)
+    dev = torch.from_numpy(packed).to(device, non_blocking=True)
     off = 2 * total
     return CompactionInputs(
         req_offsets=dev[off : off + 2 * len(offsets)].view(torch.int64),
@@ -304,10 +305,7 @@ def pack_paged_inputs(layouts, page_size, device):
     at += 2 * bases.size
     if total:
         packed[at:].view(np.uint8)[:total] = np.concatenate(keeps).astype(np.uint8)
-    host = torch.from_numpy(packed)
-    if torch.cuda.is_available():
-        host = host.pin_memory()
-    dev = host.to(device, non_blocking=True)
+    dev = torch.from_numpy(packed).to(device, non_blocking=True)
     return PagedInputs(
         req_offsets=dev[at_off : at_off + 2 * (B + 1)].view(torch.int64),
         keep=dev[at:].view(torch.uint8)[:total],

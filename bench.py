@@ -375,6 +375,65 @@ def cow_config(device, flush):
     }
 
 
+def multistage_config(device, flush):
+    """A 6-turn agent prompt of 32768 tokens compiled in one prefill (1-2
+    dropped tool spans of 500-2000 tokens per turn boundary): host layout and
+    occurrence-window compile (C++), then the device binding of every
+    occurrence (slots, copies, terminal row, retired slots; 2 launches) and
+    the all-layer Reposition of the copies."""
+    from akv_amd import occurrence as ow
+    from akv_amd import plan
+
+    n = 32768
+    events, visible = synth.trajectory_events(n, 6, 500, 2000, seed=6)
+    t0 = time.perf_counter()
+    lay = plan.compile_context_layout(**events)
+    t1 = time.perf_counter()
+    window = ow.compile_occurrence_window(lay, visible, lay.positions, query_start=0, query_end=n)
+    t2 = time.perf_counter()
+    keep = np.asarray(lay.keep_mask, dtype=bool)
+    inp = ow.pack_final_forward([window], [keep], device)
+    t3 = time.perf_counter()
+    out = ow.allocate_final_forward_outputs(inp, device)
+    m = synth.GPT_OSS_120B
+    pool_slots = n + inp.extra[0] + 1
+    rng = np.random.default_rng(6)
+    perm = rng.permutation(np.arange(1, pool_slots)).astype(np.int32)
+    birth = torch.from_numpy(perm[:n]).to(device)
+    fresh = torch.from_numpy(perm[n:]).to(device)
+    table = torch.full((1, n + 8), -1, dtype=torch.int32, device=device)
+    rows = torch.zeros(1, dtype=torch.int64, device=device)
+    pool = synth.make_pool(m, pool_slots, device, seed=6, generate_on_device=True)
+    w = synth.Workload("trajectory", m, (n,), ((),), 6, 2 * n, pool_slots)
+    rope = synth.rope_table(w, device)
+
+    def bind():
+        ow.bind_final_forward(inp, table, rows, birth, fresh, out)
+
+    def repo():
+        ops.reposition_kv_layers(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], out.copy_src, out.copy_dst,
+                                 out.copy_pairs, rope)
+
+    bind()
+    warm_bind, cold_bind = _time_steps(bind, 50, 5, 20, flush)
+    warm_repo, _ = _time_steps(repo, 20, 3, 0, flush)
+    copies = inp.extra[0]
+    alg = copies * (4 * m.n_layers * m.n_heads * m.head_dim * 2 + 16 + 2 * m.rotary_dim * 4)
+    del pool
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"gpt-oss-120b 6-turn trajectory, {n} tokens, one prefill",
+        "kept": int(keep.sum()), "occurrences": window.occurrence_count, "segments": window.segment_count,
+        "copies": copies,
+        "host_layout_compile_ms": round((t1 - t0) * 1e3, 2), "host_window_compile_ms": round((t2 - t1) * 1e3, 2),
+        "host_pack_ms": round((t3 - t2) * 1e3, 2),
+        "bind_ms_back_to_back": round(warm_bind, 5), "bind_p50_ms": round(percentile(cold_bind, 50), 5),
+        "reposition_ms": round(warm_repo, 4),
+        "reposition_pct_hbm_peak": round(100 * alg / (warm_repo / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
+        "kernel_launches": {"bind": 2, "reposition": 1},
+    }
+
+
 def prefill_config(device, flush, extend=4096):
     """Next turn's prefill over the compacted 32k GPT-OSS request: 4096 new
     tokens attend to the 19441 kept tokens (positions with the dropped holes)
@@ -631,7 +690,7 @@ def main():
         print("# secondary configurations ...", file=sys.stderr, flush=True)
         result["other_configs"] = [tiny_config(device, pipe.flush), ascending_slots_config(device, pipe.flush),
                                    ragged_config(device, pipe.flush), decode_consumer_config(device, pipe.flush),
-                                   prefill_config(device, pipe.flush)]
+                                   prefill_config(device, pipe.flush), multistage_config(device, pipe.flush)]
         if not args.no_cow:
             print("# copy-on-write configuration ...", file=sys.stderr, flush=True)
             result["other_configs"].append(cow_config(device, pipe.flush))
