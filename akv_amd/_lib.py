@@ -75,6 +75,10 @@ _SIGNATURES = {
         [c_int32, _P, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, _P, _P,
          c_int64, _P],
     ),
+    "akv_copy_kv_rows": (
+        c_int32,
+        [_P, _P, _P, _P, c_int32, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, c_int64, _P],
+    ),
     "akv_window_count": (
         c_int32,
         [c_int64, _P, _P, _P, c_int64, _P, _P, _P, _P, _P, c_int64, c_int64, _P],

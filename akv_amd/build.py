@@ -24,7 +24,7 @@ ARCH = "gfx950"
 
 HIP_SOURCES = [
     "common.hip", "reposition.hip", "compact.hip", "compact_pages.hip", "decode_meta.hip", "decode_attention.hip",
-    "context_attention.hip", "bind_occurrences.hip",
+    "context_attention.hip", "bind_occurrences.hip", "kv_transfer.hip",
 ]
 CXX_SOURCES = ["event_plan.cpp", "occurrence_window.cpp"]
 

@@ -121,7 +121,9 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
   const int32_t t0 = static_cast<int32_t>(blockIdx.x) * T;
   if (t0 >= qlen) return;
   const int64_t kv0 = load_index(a.kv_indptr, i64, seg);
-  const int32_t plen = static_cast<int32_t>(load_index(a.kv_indptr, i64, seg + 1) - kv0);
+  // without prefix indices there is no prefix, whatever kv_indptr says
+  const int32_t plen =
+      a.kv_indices ? static_cast<int32_t>(load_index(a.kv_indptr, i64, seg + 1) - kv0) : 0;
   // segment-local views
   const PosT* qpos = static_cast<const PosT*>(a.q_pos) + qo0;
   const PosT* kpos = static_cast<const PosT*>(a.kv_pos) + kv0;

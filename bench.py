@@ -7,13 +7,17 @@ Reposition.  Synthetic data; all inputs resident in HBM before timing.
 
 One step = the whole GPU side of the hot path: page-table compaction
 (terminal row, freed slots, copy lists, decode layout, kv_indptr /
-kv_indices; 3 kernels) -> all-layer Reposition (K re-rotation + V move, one
+kv_indices; 2 kernels) -> all-layer Reposition (K re-rotation + V move, one
 launch).  ``value`` = retained-KV bytes moved (K and V, read + write) per
 step / step time over K back-to-back steps.  Also reported: the Reposition
 kernel's average launch in that timed region and its roofline against
 8 TB/s; p50 / p99 latency of the step and of the Reposition alone after a
 1 GiB read flush of L2 + the 256 MB MALL; the CPU oracle on a bounded sample
-of the same workload.
+of the same workload.  ``other_configs`` measures the surrounding rows on
+their own workloads: the tiny and ragged-batch compactions, ascending slots,
+the decode step over the compacted metadata, the next turn's prefill
+attention, a multi-turn trajectory's occurrence binding, the compacted
+handoff copies and the page-16 copy-on-write batch.
 """
 
 import argparse
@@ -434,6 +438,46 @@ def multistage_config(device, flush):
     }
 
 
+def handoff_config(device, flush):
+    """Compacted final-version handoff of the 32k GPT-OSS request: its 19441
+    active rows x 36 layers (K and V) packed into a contiguous buffer (P
+    side), unpacked into fresh owners of a second pool (D side), and copied
+    pool to pool directly (the single-GPU stand-in for peer writes)."""
+    from akv_amd import transfer
+
+    m = synth.GPT_OSS_120B
+    w = synth.workload("gpt-oss-32k")
+    kept = int(synth.compile_layouts(w)[0].keep_mask.sum())
+    rng = np.random.default_rng(8)
+    src_pool = synth.make_pool(m, w.pool_slots, device, seed=8, generate_on_device=True)
+    dst_pool = synth.make_pool(m, w.pool_slots, device, seed=9, generate_on_device=True)
+    active = torch.from_numpy(rng.choice(np.arange(1, w.pool_slots), kept, replace=False).astype(np.int32)).to(device)
+    owners = torch.from_numpy(rng.choice(np.arange(1, w.pool_slots), kept, replace=False).astype(np.int32)).to(device)
+    packed = transfer.PackedKV.empty(m.n_layers, kept, m.n_heads, m.head_dim, m.dtype, device)
+
+    def pack():
+        transfer.pack_active_kv(src_pool.k_ptrs, src_pool.v_ptrs, src_pool.k[0], active, packed)
+
+    def unpack():
+        transfer.unpack_active_kv(packed, dst_pool.k_ptrs, dst_pool.v_ptrs, dst_pool.k[0], owners)
+
+    def direct():
+        transfer.copy_kv_rows(src_pool.k_ptrs, src_pool.v_ptrs, src_pool.k[0], dst_pool.k_ptrs, dst_pool.v_ptrs,
+                              dst_pool.k[0], kept, src_slots=active, dst_slots=owners)
+
+    moved = kept * m.n_layers * 2 * m.n_heads * m.head_dim * 2 * 2  # read + write
+    out = {"workload": f"{w.name} active rows ({kept} tokens x {m.n_layers} layers, K and V)",
+           "bytes_per_copy": moved}
+    for name, fn in (("pack", pack), ("unpack", unpack), ("pool_to_pool", direct)):
+        warm, _ = _time_steps(fn, 20, 3, 0, flush)
+        out[f"{name}_ms"] = round(warm, 4)
+        out[f"{name}_pct_hbm_peak"] = round(100 * moved / (warm / 1e3) / 1e9 / HBM_PEAK_GBS, 2)
+    del src_pool, dst_pool, packed
+    torch.cuda.empty_cache()
+    out["kernel_launches_per_copy"] = 1
+    return out
+
+
 def prefill_config(device, flush, extend=4096):
     """Next turn's prefill over the compacted 32k GPT-OSS request: 4096 new
     tokens attend to the 19441 kept tokens (positions with the dropped holes)
@@ -690,7 +734,8 @@ def main():
         print("# secondary configurations ...", file=sys.stderr, flush=True)
         result["other_configs"] = [tiny_config(device, pipe.flush), ascending_slots_config(device, pipe.flush),
                                    ragged_config(device, pipe.flush), decode_consumer_config(device, pipe.flush),
-                                   prefill_config(device, pipe.flush), multistage_config(device, pipe.flush)]
+                                   prefill_config(device, pipe.flush), multistage_config(device, pipe.flush),
+                                   handoff_config(device, pipe.flush)]
         if not args.no_cow:
             print("# copy-on-write configuration ...", file=sys.stderr, flush=True)
             result["other_configs"].append(cow_config(device, pipe.flush))

@@ -360,6 +360,26 @@ int akv_bind_occurrences(int32_t n_requests, const int64_t* bases,
                          int64_t workspace_bytes, void* stream);
 
 /*
+ * All-layer K and V row copy between two slot spaces: for token t and
+ * layer l, the row_bytes-long K row (and V row) at slot src_slots[t] of
+ * src_k_ptrs[l] (src_v_ptrs[l]) goes to slot dst_slots[t] of dst_k_ptrs[l]
+ * (dst_v_ptrs[l]); a NULL slot vector means slot t (a packed buffer).
+ * Pointer tables are DEVICE arrays of n_layers base addresses; strides are
+ * bytes between slots; rows, strides and bases are 16-byte aligned.
+ * Destinations may be peer-GPU addresses.  Replaces the compacted
+ * final-version transfer's gather/scatter of request_active_slots and the
+ * D-side destination fill, akv/system/sglang/srt/disaggregation/
+ * context_transfer.py:110-128,201-259 (the transport itself is external).
+ */
+int akv_copy_kv_rows(const uint64_t* src_k_ptrs, const uint64_t* src_v_ptrs,
+                     const uint64_t* dst_k_ptrs, const uint64_t* dst_v_ptrs,
+                     int32_t n_layers, int64_t row_bytes,
+                     int64_t src_k_stride, int64_t src_v_stride,
+                     int64_t dst_k_stride, int64_t dst_v_stride,
+                     const int32_t* src_slots, const int32_t* dst_slots,
+                     int64_t n_tokens, void* stream);
+
+/*
  * Host event compiler (CPU, no device work).  Replays Drop and Reposition
  * events over the raw token stream.  Two calls, like the reference's count
  * and fill passes: akv_plan_count returns the number of transitions through
