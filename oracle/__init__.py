@@ -1,7 +1,7 @@
 """CPU oracle for the Drop + Reposition hot path -- TEST INFRASTRUCTURE ONLY.
 
 This package restates, on the CPU, what the reference computes on the path
-that the HIP library replaces.  It is the checker: only ``tests/``,
+that the HIP library replaces, to check it: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it.  The product (``akv_amd``) never imports, links or calls anything
 here, and it has no CPU fallback: when the HIP library is missing it raises.
