@@ -677,6 +677,22 @@ def main():
         repo_ms.append(e1.elapsed_time(e2))
     print(f"# latency iterations done: {args.latency_iters}", file=sys.stderr, flush=True)
 
+    # the same launch with every pair at its birth position: a pure row copy
+    # of the same slots (same bytes, no rotation) -- the access pattern's own
+    # rate, against which the rotation's cost shows
+    copy_only = None
+    if not args.reposition_only:
+        o, p, neox = pipe.out, pipe.pool, pipe.w.model.is_neox_style
+        same = torch.stack((o.copy_pairs[:, 0], o.copy_pairs[:, 0]), 1).contiguous()
+
+        def copy_step():
+            ops.reposition_kv_layers(p.k_ptrs, p.v_ptrs, p.k[0], p.v[0], o.copy_src, o.copy_dst, same, pipe.rope,
+                                     is_neox_style=neox)
+
+        warm_copy, _ = _time_steps(copy_step, args.steps, args.warmup, 0, pipe.flush)
+        copy_only = {"ms": round(warm_copy, 5),
+                     "pct_hbm_peak": round(100 * pipe.alg_bytes / (warm_copy / 1e3) / 1e9 / HBM_PEAK_GBS, 2)}
+
     # roofline of the dominant kernel: its average launch inside the timed
     # (back-to-back, steady-state) region
     repo_avg_s = float(np.mean(repo_timed_ms)) / 1e3
@@ -715,6 +731,8 @@ def main():
         "reposition_p50_ms": round(percentile(repo_ms, 50), 5),
         "reposition_p99_ms": round(percentile(repo_ms, 99), 5),
         "reposition_steady_ms": round(float(np.mean(repo_timed_ms)), 5),
+        # same slots, pairs at the birth position (a bit copy, no rotation)
+        "reposition_copy_only": copy_only,
         "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         # compaction: count + scatter (one request spans 128 tiles, under the
         # fused-offsets limit) ; Reposition: one launch for the 36-layer group
