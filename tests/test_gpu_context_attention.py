@@ -84,6 +84,28 @@ def test_segments_match_oracle(device, d, hq, hkv, window, positions, with_sinks
             assert err <= TOL, f"segment {s} (q {Q_LENS[s]}, prefix {P_LENS[s]}) max err {err}"
 
 
+@pytest.mark.parametrize("idx_dtype,pos_dtype,indptr_dtype", [(torch.int64, torch.int32, torch.int32),
+                                                              (torch.int32, torch.int32, torch.int64)])
+def test_index_dtypes(device, idx_dtype, pos_dtype, indptr_dtype):
+    """int32 / int64 indices, positions and indptrs take their own kernel paths."""
+    d, hq, hkv = 64, 16, 2
+    c = _case(device, hq, hkv, d, [33, 70], [100, 9], seed=31)
+    dv = c["dev"]
+    qo = torch.from_numpy(c["qo"]).to(indptr_dtype).to(device)
+    kv = torch.from_numpy(c["kv"]).to(indptr_dtype).to(device)
+    idx = torch.from_numpy(c["idx"]).to(idx_dtype).to(device)
+    qp = torch.from_numpy(c["qpos"]).to(pos_dtype).to(device)
+    kp = torch.from_numpy(c["kpos"]).to(pos_dtype).to(device)
+    out = torch.empty(dv["q"].shape, dtype=torch.float32, device=device)
+    ca.extend_attention_fwd(dv["q"], dv["ke"], dv["ve"], out, dv["kp"], dv["vp"], qo, kv, idx, None, True, None, 70,
+                            sm_scale=0.125, sliding_window_size=16, context_q_positions=qp, context_kv_positions=kp)
+    torch.cuda.synchronize()
+    want = oat.context_attention(_f32(c["q"]), _f32(c["ke"]), _f32(c["ve"]), _f32(c["kp"]), _f32(c["vp"]),
+                                 c["qo"], c["kv"], c["idx"], 0.125, window=16, q_positions=c["qpos"],
+                                 kv_positions=c["kpos"])
+    assert np.abs(_f32(out) - want).max() <= TOL
+
+
 def test_metadata_path_ordinary_sequences(device):
     """ContextSequence.ordinary -> ContextAttentionPlan.merge/bind -> forward."""
     hq, hkv, d = 64, 8, 64
