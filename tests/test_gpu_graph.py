@@ -81,3 +81,62 @@ def test_graph_replays_match_eager(device):
         for t, x in zip(pool.k + pool.v, want_kv):
             assert torch.equal(t[dst].view(torch.int16), x.view(torch.int16)), f"replay {replay}"
     assert np.array_equal(kv.cpu().numpy(), out.kv_indices.cpu().numpy())
+
+
+def test_graph_replays_attention_consumers(device):
+    """Decode attention (with its workspace) and the prefill attention over
+    fixed metadata captured in one graph: replays equal the eager outputs."""
+    from akv_amd import attention
+    from akv_amd import context_attention as ca
+
+    g = torch.Generator(device=device).manual_seed(21)
+    hq, hkv, d = 64, 8, 64
+    slots = 6000
+    k = torch.randn((slots, hkv, d), generator=g, device=device).to(torch.bfloat16)
+    v = torch.randn((slots, hkv, d), generator=g, device=device).to(torch.bfloat16)
+    rng = np.random.default_rng(21)
+    lengths = [300, 1, 2000, 57]
+    indptr = torch.tensor(np.concatenate(([0], np.cumsum(lengths))), dtype=torch.int32, device=device)
+    idx = torch.from_numpy(rng.integers(1, slots, size=sum(lengths)).astype(np.int32)).to(device)
+    q = torch.randn((len(lengths), hq, d), generator=g, device=device).to(torch.bfloat16)
+    sinks = torch.randn(hq, generator=g, device=device)
+    o_dec = torch.empty_like(q)
+    ws = torch.empty(attention.workspace_bytes(len(lengths), hkv, d, max(lengths)) // 4 + 1, dtype=torch.float32,
+                     device=device)
+    plan = ca.ContextAttentionPlan.merge([ca.ContextSequence.ordinary(500, 77), ca.ContextSequence.ordinary(0, 30)])
+    occ = torch.from_numpy(rng.permutation(np.arange(1, slots))[: plan.occurrence_count].astype(np.int64)).to(device)
+    meta = plan.bind(occ)
+    nq = meta.query_count
+    qe = torch.randn((nq, hq, d), generator=g, device=device).to(torch.bfloat16)
+    ke = torch.randn((nq, hkv, d), generator=g, device=device).to(torch.bfloat16)
+    ve = torch.randn((nq, hkv, d), generator=g, device=device).to(torch.bfloat16)
+    o_pre = torch.empty_like(qe)
+    torch.cuda.synchronize()
+
+    def step():
+        attention.decode_attention(q, k, v, indptr, idx, o_dec, scale=0.125, max_len=max(lengths), sinks=sinks,
+                                   workspace=ws)
+        meta.forward(ca.extend_attention_fwd, qe, ke, ve, o_pre, k, v, sm_scale=0.125, sliding_window_size=64,
+                     sinks=sinks)
+
+    step()
+    torch.cuda.synchronize()
+    want = [o_dec.clone(), o_pre.clone()]
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        step()
+    for replay in range(4):
+        o_dec.fill_(3.0)
+        o_pre.fill_(3.0)
+        ws.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o_dec.view(torch.int16), want[0].view(torch.int16)), f"replay {replay}"
+        assert torch.equal(o_pre.view(torch.int16), want[1].view(torch.int16)), f"replay {replay}"
