@@ -11,9 +11,10 @@
 // 201-259), and a direct pool-to-pool copy -- to a peer GPU's pool when the
 // destination pointers are peer (xGMI) addresses.
 //
-// Work item = one 16-byte chunk; a workgroup takes kTokens tokens x all
-// layers x {K, V} x row chunks and keeps kBatch independent loads in
-// flight per thread before storing them.
+// Rows of an even number of 16-byte chunks (up to 2 KiB): a workgroup per
+// token with layer rows side by side, double-buffered over the layers (the
+// Reposition's structure without the rotation).  Other sizes: flat 16-byte
+// work items, kBatch independent loads in flight per thread.
 #include "common.h"
 
 namespace akv {
@@ -73,6 +74,50 @@ __global__ void __launch_bounds__(kThreads) copy_kv_rows_kernel(const CopyArgs a
   }
 }
 
+// Row-structured variant for rows of an even number of chunks (at most 128):
+// a workgroup per token, `rows` layer rows side by side, each lane moving
+// chunks j and j + lanes of the K and the V row; the next layer's loads are
+// in flight while this layer is stored.
+struct RowChunks {
+  u32x4 k0, k1, v0, v1;
+};
+
+__global__ void __launch_bounds__(1024) copy_kv_rows_vec_kernel(const CopyArgs a, int lanes, int rows) {
+  const int64_t t = blockIdx.x;
+  const int sub = threadIdx.x / lanes;
+  const int j = threadIdx.x - sub * lanes;
+  if (sub >= rows || t >= a.n) return;
+  const int64_t s = a.src_slots ? a.src_slots[t] : t;
+  const int64_t d = a.dst_slots ? a.dst_slots[t] : t;
+  auto load = [&](int l) {
+    const char* k = reinterpret_cast<const char*>(a.src_k[l]) + s * a.src_k_stride + 16 * j;
+    const char* v = reinterpret_cast<const char*>(a.src_v[l]) + s * a.src_v_stride + 16 * j;
+    RowChunks r;
+    r.k0 = *((const global_u32x4*)k);
+    r.k1 = *((const global_u32x4*)(k + 16 * lanes));
+    r.v0 = *((const global_u32x4*)v);
+    r.v1 = *((const global_u32x4*)(v + 16 * lanes));
+    return r;
+  };
+  auto store = [&](int l, const RowChunks& r) {
+    char* k = reinterpret_cast<char*>(a.dst_k[l]) + d * a.dst_k_stride + 16 * j;
+    char* v = reinterpret_cast<char*>(a.dst_v[l]) + d * a.dst_v_stride + 16 * j;
+    *((global_u32x4*)k) = r.k0;
+    *((global_u32x4*)(k + 16 * lanes)) = r.k1;
+    *((global_u32x4*)v) = r.v0;
+    *((global_u32x4*)(v + 16 * lanes)) = r.v1;
+  };
+  if (sub >= a.n_layers) return;
+  RowChunks cur = load(sub);
+  for (int l = sub; l < a.n_layers; l += rows) {
+    const int next = l + rows;
+    RowChunks nxt = cur;
+    if (next < a.n_layers) nxt = load(next);
+    store(l, cur);
+    cur = nxt;
+  }
+}
+
 }  // namespace
 }  // namespace akv
 
@@ -105,7 +150,20 @@ extern "C" int akv_copy_kv_rows(const uint64_t* src_k_ptrs, const uint64_t* src_
   a.n = n_tokens;
   a.n_layers = n_layers;
   a.chunks = static_cast<int32_t>(row_bytes / 16);
-  // about 16 chunks per thread per workgroup
+  if (a.chunks % 2 == 0 && a.chunks <= 128) {
+    // one workgroup per token, ~192 threads: layer rows side by side,
+    // balanced over the passes
+    const int lanes = a.chunks / 2;
+    int rows = 192 / lanes < 1 ? 1 : 192 / lanes;
+    if (rows > n_layers) rows = n_layers;
+    const int passes = (n_layers + rows - 1) / rows;
+    rows = (n_layers + passes - 1) / passes;
+    if (n_tokens > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_copy_kv_rows: too many tokens");
+    hipLaunchKernelGGL(copy_kv_rows_vec_kernel, dim3(static_cast<unsigned>(n_tokens)), dim3(lanes * rows), 0,
+                       as_stream(stream), a, lanes, rows);
+    return check_launch("akv_copy_kv_rows");
+  }
+  // any other row size: flat 16-byte work items, about 16 per thread
   const int64_t per_token = static_cast<int64_t>(n_layers) * 2 * a.chunks;
   int64_t tokens = (static_cast<int64_t>(kThreads) * 16 + per_token - 1) / per_token;
   a.tokens_per_block = static_cast<int32_t>(tokens < 1 ? 1 : (tokens > 4096 ? 4096 : tokens));
