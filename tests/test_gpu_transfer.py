@@ -73,3 +73,26 @@ def test_validation(device):
     with pytest.raises(ValueError, match="int32"):
         transfer.copy_kv_rows(kp, vp, ks[0], kp, vp, ks[0], 4, src_slots=torch.zeros(4, dtype=torch.int64,
                                                                                     device=device))
+
+
+@pytest.mark.parametrize("layers,heads,dim", [(37, 8, 64), (5, 1, 8), (4, 3, 40), (3, 16, 128), (2, 1, 1024)])
+def test_row_sizes_and_layer_counts(device, layers, heads, dim):
+    """Rows of 1, 15, 64, 128 and 256 16-byte chunks: the per-token kernel
+    (even chunk counts up to 128, layer rows side by side over uneven passes)
+    and the flat kernel (any other size) copy the same rows."""
+    slots = 3000
+    ks, vs, kp, vp = _pool(device, layers, slots, heads, dim, seed=layers + dim)
+    ks2, vs2, kp2, vp2 = _pool(device, layers, slots, heads, dim, seed=layers + dim + 1)
+    rng = np.random.default_rng(dim)
+    n = 1234
+    src = torch.from_numpy(rng.choice(slots, size=n, replace=False).astype(np.int32)).to(device)
+    dst = torch.from_numpy(rng.choice(slots, size=n, replace=False).astype(np.int32)).to(device)
+    before = [t.clone() for t in vs2]
+    transfer.copy_kv_rows(kp, vp, ks[0], kp2, vp2, ks2[0], n, src_slots=src, dst_slots=dst)
+    torch.cuda.synchronize()
+    untouched = torch.ones(slots, dtype=torch.bool, device=device)
+    untouched[dst.long()] = False
+    for l in range(layers):
+        assert torch.equal(_bits(ks2[l][dst.long()]), _bits(ks[l][src.long()])), f"layer {l} K"
+        assert torch.equal(_bits(vs2[l][dst.long()]), _bits(vs[l][src.long()])), f"layer {l} V"
+        assert torch.equal(_bits(vs2[l][untouched]), _bits(before[l][untouched])), f"layer {l} V untouched"
