@@ -28,6 +28,10 @@ reference repository root):
 ``attention``   one GQA decode step with attention sinks, the consumer of the
                 compacted metadata (sink normalisation of
                 ``akv/system/sglang/srt/layers/attention/context_backend.py:254-272``).
+``ownership``   request-local page ownership across prefill forwards (chunked
+                prefill, borrowed prefixes, recovery gaps, publication):
+                ``plan_occurrence_materialization`` and ``OccurrenceState``
+                (``akv/system/sglang/srt/context_system/occurrence.py:341-920``).
 ``paging``      page-granular Drop + Reposition with copy-on-write; the
                 reference rejects page sizes other than 1
                 (``context_reposition.py:153-154``), so this module is the

@@ -26,8 +26,14 @@ from itertools import pairwise
 import numpy as np
 
 
-def compile_window(layout, visible_until):
-    """Occurrence window over the whole prompt (query_start=0, query_end=n)."""
+def compile_window(layout, visible_until, query_start=0, query_end=None):
+    """Occurrence window of the queries ``[query_start, query_end)``.
+
+    Occurrences ``[0, n)`` are the birth versions of every raw token; then,
+    segment by segment, the versions a query reads that differ from the last
+    materialised one; last the terminal versions that still differ.  Segments
+    split each stage's queries wherever a token's visibility ends.
+    """
     birth = layout.birth_positions.astype(np.int64)
     stages = layout.birth_stages.astype(np.int64)
     offsets = layout.transition_offsets.astype(np.int64)
@@ -35,6 +41,10 @@ def compile_window(layout, visible_until):
     new = layout.transition_new_positions.astype(np.int64)
     expiry = np.asarray(visible_until, dtype=np.int64)
     n = len(birth)
+    if query_end is None:
+        query_end = n
+    if not 0 <= query_start < query_end <= n:
+        raise ValueError("Occurrence query window is outside the raw prompt.")
     stage_count = len(offsets) - 1
     raw = np.arange(n, dtype=np.int64)
     if np.any(expiry <= raw):
@@ -62,7 +72,8 @@ def compile_window(layout, visible_until):
         if stage:
             lo, hi = int(offsets[stage - 1]), int(offsets[stage])
             current_pos[changed[lo:hi]] = new[lo:hi]
-        a, b = int(bounds[stage]), min(n, int(bounds[stage + 1]))
+        a = max(query_start, int(bounds[stage]))
+        b = min(query_end, int(bounds[stage + 1]))
         if a >= b:
             continue
         inner = expiry[:b]
@@ -86,6 +97,9 @@ def compile_window(layout, visible_until):
         "birth": raw,
         "terminal": current_ids,
         "keys": np.concatenate(keys) if keys else np.zeros(0, np.int64),
+        "starts": np.asarray(starts, dtype=np.int64),
+        "ends": np.asarray(ends, dtype=np.int64),
+        "key_offsets": np.asarray(key_offsets, dtype=np.int64),
     }
 
 

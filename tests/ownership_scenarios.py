@@ -1,0 +1,321 @@
+"""Seeded request lifecycles for the ownership planner tests.
+
+A scenario is one request: a random multi-stage Drop/Reposition program,
+an optional matched prefix borrowed from the cache (some pages evicted,
+an exact-prefix boundary, SWA residency), its prompt computed in 1-4
+forwards, possibly a resident recovery gap borrowed between two forwards,
+then the publication of its terminal versions and a Drop of borrowed raw
+tokens.  ``run(scenario, impl)`` drives an implementation through it with
+a lowest-first slot allocator that recycles retired slots, and returns a
+flat trace of every input and output -- the same trace for every correct
+implementation, so traces of the reference module (golden vectors), the
+oracle and the native planner compare array for array.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import events as ev
+
+INF = 2**31 - 1
+CACHE_BASE = 1_000_000  # cache-owned (borrowed) slots live above this
+
+
+def _program(rng, n):
+    k = int(rng.integers(1, 4))
+    inserts = np.sort(rng.choice(np.arange(3, n), size=min(k, n - 3), replace=False))
+    drops, offsets, drop_at = [], [0], []
+    visible = np.full(n, INF, dtype=np.int64)
+    lo = 0
+    for at in inserts:
+        if rng.random() < 0.8:
+            s = int(rng.integers(lo, max(lo + 1, at - 1)))
+            e = int(min(at, s + rng.integers(1, 6)))
+            if s < e and (not drops or s >= drops[-1]):
+                drops += [s, e]
+                visible[s:e] = np.minimum(visible[s:e], at)
+                offsets.append(len(drops) // 2)
+                drop_at.append(int(at))
+        lo = int(at)
+    events = dict(
+        token_ids=np.arange(n, dtype=np.int64),
+        drop_insert_offsets=np.asarray(drop_at, dtype=np.int64),
+        drop_range_offsets=np.asarray(offsets, dtype=np.int64),
+        drop_ranges=np.asarray(drops, dtype=np.int64),
+        reposition_raw_boundaries=(inserts - 1).astype(np.int64),
+        reposition_insert_offsets=inserts.astype(np.int64),
+    )
+    return events, visible
+
+
+def make(seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(10, 90))
+    while True:  # redraw programs whose Reposition finds no active token
+        events, visible = _program(rng, n)
+        try:
+            layout = ev.compile_context_layout(*(np.asarray(events[k]) for k in events))
+            break
+        except ValueError:
+            continue
+    sc = dict(seed=seed, n=n, layout=layout, visible=np.minimum(visible, INF).astype(np.int32))
+    m = int(rng.integers(1, n - 1)) if rng.random() < 0.5 else 0
+    cache = CACHE_BASE + rng.permutation(4 * n)
+    positions = np.asarray(layout.positions if rng.random() < 0.7 else layout.birth_positions)
+    resident = np.ones(n, dtype=bool)
+    if rng.random() < 0.3:
+        resident[rng.random(n) < 0.1] = False
+    swa = rng.random(n) < 0.8 if rng.random() < 0.5 else None
+    sc["match"] = dict(slots=cache[:n].astype(np.int64), positions=positions.astype(np.int32), resident=resident,
+                       length=m, exact=int(rng.integers(0, m + 1)), swa=swa)
+    cuts = sorted(set(int(c) for c in rng.integers(m + 1, n, size=int(rng.integers(0, 4))))) if m + 1 < n else []
+    bounds = [m, *[c for c in cuts if m < c < n], n]
+    # a recovery gap: the head of one forward's range is borrowed instead
+    gap = None
+    if rng.random() < 0.4:
+        i = int(rng.integers(0, len(bounds) - 1))
+        a, b = bounds[i], bounds[i + 1]
+        if b - a >= 2:
+            gap = (a, int(rng.integers(a + 1, b)))
+    sc["forwards"] = bounds
+    sc["gap"] = gap
+    sc["gap_exact_bump"] = bool(rng.random() < 0.5)
+    # chunked prefill publishes every finished chunk to the cache (which may
+    # dedup a private page against a cached copy) and drops the borrowed
+    # owners no later query needs
+    sc["publish_each"] = bool(rng.random() < 0.5)
+    # some lifecycles drop borrowed owners of tokens later queries still
+    # read (their private terminal copies then become the copy sources)
+    sc["drop_needed"] = bool(rng.random() < 0.3)
+    sc["publish_replace"] = rng.random(n) < 0.3
+    sc["cache_len"] = int(rng.integers(0, n + 1)) if rng.random() < 0.3 else None
+    sc["drop"] = rng.random(n) < 0.3
+    return sc
+
+
+class Allocator:
+    """Lowest-first allocation over a recycled free set (slot 0 reserved)."""
+
+    def __init__(self):
+        self.next = 1
+        self.free = []
+
+    def take(self, k):
+        self.free.sort()
+        got = self.free[:k]
+        self.free = self.free[k:]
+        while len(got) < k:
+            got.append(self.next)
+            self.next += 1
+        return np.asarray(got, dtype=np.int64)
+
+    def release(self, slots):
+        s = [int(x) for x in slots]
+        if len(set(s)) != len(s) or set(s) & set(self.free):
+            raise AssertionError("a slot was freed twice")
+        if any(x >= CACHE_BASE for x in s):
+            raise AssertionError("a cache-owned slot was freed by the request")
+        self.free += s
+
+
+def run(sc, impl):
+    """Drive ``impl`` through the scenario; returns [(name, array)]."""
+    trace = []
+
+    def rec(name, value):
+        trace.append((name, None if value is None else np.asarray(value)))
+
+    def record_state(prefix, st):
+        for k, v in impl.fields(st).items():
+            rec(f"{prefix}.{k}", v)
+
+    layout, visible, n = sc["layout"], sc["visible"], sc["n"]
+    mt = sc["match"]
+    m = mt["length"]
+    alloc = Allocator()
+
+    def publish(prefix, st, length, cache_len, serial):
+        """Cache insert: private terminal pages may be deduplicated against
+        cached copies (the cache frees the private duplicate)."""
+        f = impl.fields(st)
+        term = impl.terminal_slots(st)
+        rows = f["terminal_rows"]
+        dedup = sc["publish_replace"][:length] & (rows >= 0)
+        dedup[rows >= 0] &= f["owned"][rows[rows >= 0]]
+        if cache_len is not None:
+            dedup[cache_len:] = False
+        cached = CACHE_BASE + 16 * n + serial * n + np.arange(length, dtype=np.int64)
+        matched = np.where(dedup, cached, term)
+        swa = None if mt["swa"] is None else sc["publish_replace"][:length] | mt["swa"][:length]
+        rec(prefix + ".matched", matched)
+        rec(prefix + ".cache_len", np.int64(-1 if cache_len is None else cache_len))
+        try:
+            st = impl.publish(st, matched, cache_len, swa)
+        except ValueError as e:
+            rec(prefix + ".error", np.frombuffer(str(e).encode(), dtype=np.uint8))
+            return None
+        alloc.release(term[dedup])
+        record_state(prefix + ".state", st)
+        return st
+
+    swa = None if mt["swa"] is None else mt["swa"][:m]
+    st = impl.from_match(mt["slots"][:m], mt["positions"][:m], mt["exact"], mt["resident"][:m], swa)
+    bounds = sc["forwards"]
+    gap = sc["gap"]
+    for f, (qs, qe) in enumerate(zip(bounds[:-1], bounds[1:])):
+        if gap is not None and qs == gap[0]:
+            exact = impl.fields(st)["exact_prefix_len"]
+            if sc["gap_exact_bump"]:
+                exact = max(exact, gap[1])
+            st = impl.gap(st, mt["slots"], mt["positions"], mt["resident"], gap[1], exact,
+                          None if mt["swa"] is None else mt["swa"])
+            record_state(f"f{f}.gap", st)
+            qs = gap[1]
+        win = impl.window(layout, visible, qs, qe)
+        for k in ("raw", "pos", "terminal", "keys", "starts", "ends", "key_offsets"):
+            rec(f"f{f}.window.{k}", win[k])
+        keep = impl.keep(st, layout, qe)
+        rec(f"f{f}.keep", keep)
+        try:
+            p = impl.plan(st, win, keep)
+        except ValueError as e:
+            rec(f"f{f}.error", np.frombuffer(str(e).encode(), dtype=np.uint8))
+            return trace
+        for k in ("source_rows", "allocated", "copy_source_rows", "pairs", "terminal_occurrences", "read_cached",
+                  "repositioned_cached"):
+            rec(f"f{f}.plan.{k}", p[k])
+        q_slots = alloc.take(qe - qs)
+        extra = alloc.take(int(p["extra_page_count"]))
+        rec(f"f{f}.query_slots", q_slots)
+        rec(f"f{f}.extra_slots", extra)
+        st, out = impl.advance(st, win, p, q_slots, extra, visible)
+        for k in ("occurrence_slots", "copy_source_slots", "copy_destination_slots", "copy_position_pairs",
+                  "retired_slots", "unused_swa_slots", "retired_swa_resident"):
+            rec(f"f{f}.adv.{k}", out[k])
+        record_state(f"f{f}.state", st)
+        alloc.release(out["retired_slots"])  # the forward completed
+        if sc["publish_each"] and qe < n:
+            st = publish(f"f{f}.pub", st, qe, qe // 2 if sc["drop_needed"] else qe, f)
+            if st is None:
+                return trace
+            keep_mask = np.asarray(layout.keep_mask[:qe], dtype=bool)
+            dropped = ~(keep_mask | (visible[:qe] > qe))
+            if sc["drop_needed"]:
+                dropped |= sc["drop"][:qe]
+            st = impl.drop(st, dropped)
+            record_state(f"f{f}.drop", st)
+    if bounds[-1] != n:
+        return trace
+    rec("terminal_slots", impl.terminal_slots(st))
+    rec("terminal_swa", impl.terminal_swa(st))
+    rec("private_slots_before_publish", impl.private(st))
+    st = publish("publish", st, n, sc["cache_len"], len(bounds))
+    if st is None:
+        return trace
+    st = impl.drop(st, sc["drop"])
+    record_state("drop.state", st)
+    rec("private_slots", impl.private(st))
+    rec("nonterminal_private_slots", impl.nonterminal(st))
+    rec("nonterminal_private_residency", impl.nonterminal_residency(st))
+    return trace
+
+
+def plan_case(seed):
+    """Direct call of the plan over arbitrary ownership metadata: random
+    presence, ownership, terminal rows, canonical positions and exact-prefix
+    boundary, so every branch is taken (including copies from a terminal
+    owner when the canonical one is gone, and missing sources)."""
+    rng = np.random.default_rng(50_000 + seed)
+    sc = make(seed)
+    n = sc["n"]
+    layout = sc["layout"]
+    qs = int(rng.integers(1, n - 1))
+    qe = int(rng.integers(qs + 1, n + 1))
+    choice = rng.integers(0, 3, size=qs)
+    cpos = np.where(choice == 0, layout.birth_positions[:qs],
+                    np.where(choice == 1, layout.positions[:qs], rng.integers(0, n, size=qs)))
+    present = rng.random(qs) < 0.7
+    return dict(sc=sc, qs=qs, qe=qe, canonical_positions=cpos.astype(np.int32),
+                canonical_present=present, canonical_owned=rng.random(qs) < 0.5,
+                terminal_present=rng.random(qs) < np.where(present, 0.5, 0.95),
+                terminal_keep=np.asarray(layout.keep_mask[:qe], dtype=bool) & (rng.random(qe) < 0.9),
+                exact=int(rng.integers(0, qs + 1)))
+
+
+def run_plan_case(case, impl):
+    sc = case["sc"]
+    win = impl.window(sc["layout"], sc["visible"], case["qs"], case["qe"])
+    trace = [("window.raw", win["raw"]), ("window.pos", win["pos"])]
+    try:
+        p = impl.plan_free(win, case["canonical_positions"], case["canonical_present"], case["canonical_owned"],
+                           case["terminal_present"], case["terminal_keep"], case["qs"], case["qe"], case["exact"])
+    except ValueError as e:
+        return trace + [("error", np.frombuffer(str(e).encode(), dtype=np.uint8))]
+    return trace + [(f"plan.{k}", np.asarray(p[k])) for k in (
+        "source_rows", "allocated", "copy_source_rows", "pairs", "terminal_occurrences", "read_cached",
+        "repositioned_cached")]
+
+
+class OracleImpl:
+    """The oracle restatement behind the scenario interface."""
+
+    def __init__(self):
+        from oracle import occurrence as occ
+        from oracle import ownership as own
+
+        self.occ, self.own = occ, own
+
+    def window(self, layout, visible, qs, qe):
+        return self.occ.compile_window(layout, visible, qs, qe)
+
+    def from_match(self, slots, positions, exact, resident, swa):
+        return self.own.State.from_match(slots, positions, exact_prefix_len=exact, resident=resident,
+                                         swa_resident=swa)
+
+    def gap(self, st, slots, positions, resident, end, exact, swa):
+        return st.reuse_match_gap(slots, positions, resident, end, exact_prefix_len=exact, swa_resident=swa)
+
+    def keep(self, st, layout, qe):
+        return st.prefill_terminal_keep(layout, qe)
+
+    def plan(self, st, win, keep):
+        return st.plan(win, keep)
+
+    def plan_free(self, win, cpos, present, owned, tpresent, keep, qs, qe, exact):
+        return self.own.plan(win, cpos, present, owned, tpresent, keep, query_start=qs, query_end=qe,
+                             exact_prefix_len=exact)
+
+    def advance(self, st, win, p, q_slots, extra, visible):
+        a = st.advance(win, p, q_slots, extra, visible)
+        return a.state, dict(occurrence_slots=a.occurrence_slots, copy_source_slots=a.copy_source_slots,
+                             copy_destination_slots=a.copy_destination_slots,
+                             copy_position_pairs=a.copy_position_pairs, retired_slots=a.retired_slots,
+                             unused_swa_slots=a.unused_swa_slots, retired_swa_resident=a.retired_swa_resident)
+
+    @staticmethod
+    def fields(st):
+        return dict(slots=st.slots, owned=st.owned, canonical_rows=st.canonical_rows,
+                    terminal_rows=st.terminal_rows, canonical_positions=st.canonical_positions,
+                    exact_prefix_len=np.int64(st.exact_prefix_len), swa_resident=st.swa_resident)
+
+    def terminal_slots(self, st):
+        return st.terminal_slots()
+
+    def terminal_swa(self, st):
+        return st.terminal_swa_residency()
+
+    def publish(self, st, matched, cache_len, swa):
+        return st.publish(matched, cache_len=cache_len, swa_resident=swa)
+
+    def drop(self, st, mask):
+        return st.drop_borrowed_raw(mask)
+
+    def private(self, st):
+        return st.private_slots()
+
+    def nonterminal(self, st):
+        return st.nonterminal_private_slots()
+
+    def nonterminal_residency(self, st):
+        return st.nonterminal_private_residency()
