@@ -79,6 +79,20 @@ _SIGNATURES = {
         c_int32,
         [_P, _P, _P, _P, c_int32, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, c_int64, _P],
     ),
+    "akv_plan_ownership": (
+        c_int32,
+        [c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+         _P, _P, _P, _P, _P],
+    ),
+    "akv_advance_ownership": (
+        c_int32,
+        [c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, c_int32, _P, c_int64, _P, _P, _P,
+         _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    ),
+    "akv_gather_slots": (
+        c_int32,
+        [c_int32, _P, c_int64, _P, _P, _P, c_int64, c_int64, _P, _P, _P],
+    ),
     "akv_window_count": (
         c_int32,
         [c_int64, _P, _P, _P, c_int64, _P, _P, _P, _P, _P, c_int64, c_int64, _P],

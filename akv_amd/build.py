@@ -24,9 +24,9 @@ ARCH = "gfx950"
 
 HIP_SOURCES = [
     "common.hip", "reposition.hip", "compact.hip", "compact_pages.hip", "decode_meta.hip", "decode_attention.hip",
-    "context_attention.hip", "bind_occurrences.hip", "kv_transfer.hip",
+    "context_attention.hip", "bind_occurrences.hip", "kv_transfer.hip", "gather_slots.hip",
 ]
-CXX_SOURCES = ["event_plan.cpp", "occurrence_window.cpp"]
+CXX_SOURCES = ["event_plan.cpp", "occurrence_window.cpp", "ownership.cpp"]
 
 COMMON_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-result"]
 HIP_FLAGS = [

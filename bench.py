@@ -438,6 +438,107 @@ def multistage_config(device, flush):
     }
 
 
+CHUNKS = 4
+
+
+def _chunked_lifecycle(device, lay, visible, n, chunks, slot_perm, on_copies=None, timings=None):
+    """One request prefilled in ``chunks`` forwards with per-chunk cache
+    publication: window (C++), plan (C++), slot allocation, advance (C++ +
+    one gather launch), the chunk's Reposition (``on_copies``), publication
+    (one gather launch).  Returns the final state."""
+    from akv_amd import occurrence as ow
+    from akv_amd import ownership as own
+
+    state = own.OccurrenceState.from_match(torch.empty(0, dtype=torch.int64, device=device),
+                                           torch.empty(0, dtype=torch.int32), exact_prefix_len=0)
+    next_slot = 0
+    bounds = np.linspace(0, n, chunks + 1).astype(int)
+    for qs, qe in zip(bounds[:-1], bounds[1:]):
+        t0 = time.perf_counter()
+        window = ow.compile_occurrence_window(lay, visible, lay.positions, query_start=int(qs), query_end=int(qe))
+        t1 = time.perf_counter()
+        plan = state.plan(window, state.prefill_terminal_keep(lay, int(qe)))
+        t2 = time.perf_counter()
+        q = slot_perm[next_slot : next_slot + qe - qs]
+        extra = slot_perm[next_slot + qe - qs : next_slot + qe - qs + plan.extra_page_count]
+        next_slot += qe - qs + plan.extra_page_count
+        adv = state.advance(window, plan, q, extra, visible)
+        t3 = time.perf_counter()
+        if on_copies is not None:
+            on_copies(adv)
+        state = adv.state
+        t4 = time.perf_counter()
+        if qe < n:
+            state = state.publish(state.terminal_slots(), cache_len=int(qe))
+        t5 = time.perf_counter()
+        if timings is not None:
+            timings.append(dict(window=t1 - t0, plan=t2 - t1, advance=t3 - t2, publish=t5 - t4,
+                                copies=int(plan.extra_page_count), occurrences=window.occurrence_count))
+    return state
+
+
+def chunked_config(device, flush):
+    """The same 6-turn 32768-token trajectory prefilled in 4 chunks of 8192
+    with per-chunk cache publication (chunked prefill over the radix cache):
+    per chunk the host window / plan / advance (C++), one gather launch for
+    every slot list of the forward, the Reposition of its copies and one
+    gather launch for the publication."""
+    from akv_amd import plan as lp
+
+    n = 32768
+    events, visible = synth.trajectory_events(n, 6, 500, 2000, seed=6)
+    lay = lp.compile_context_layout(**events)
+    m = synth.GPT_OSS_120B
+    pool_slots = 3 * n
+    rng = np.random.default_rng(7)
+    perm = torch.from_numpy(rng.permutation(np.arange(1, pool_slots)).astype(np.int64)).to(device)
+    pool = synth.make_pool(m, pool_slots, device, seed=7, generate_on_device=True)
+    w = synth.Workload("trajectory", m, (n,), ((),), 6, 2 * n, pool_slots)
+    rope = synth.rope_table(w, device)
+    repo_ms, copies = [], []
+
+    def reposition(adv):
+        if len(adv.copy_source_slots):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            ops.reposition_kv_layers(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], adv.copy_source_slots,
+                                     adv.copy_destination_slots, adv.copy_position_pairs, rope)
+            e.record()
+            repo_ms.append((s, e))
+            copies.append(len(adv.copy_source_slots))
+
+    _chunked_lifecycle(device, lay, visible, n, CHUNKS, perm)  # warm-up
+    torch.cuda.synchronize()
+    runs = []
+    for _ in range(5):
+        timings = []
+        repo_ms.clear()
+        copies.clear()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        final = _chunked_lifecycle(device, lay, visible, n, CHUNKS, perm, reposition, timings)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        runs.append((wall, timings, [a.elapsed_time(b) for a, b in repo_ms], list(copies)))
+    wall, timings, repo, ncopies = sorted(runs, key=lambda r: r[0])[len(runs) // 2]
+    term = final.terminal_slots()
+    kept = int((term >= 0).sum())
+    alg = sum(ncopies) * (4 * m.n_layers * m.n_heads * m.head_dim * 2 + 16 + 2 * m.rotary_dim * 4)
+    del pool
+    torch.cuda.empty_cache()
+    ms = lambda key: [round(t[key] * 1e3, 3) for t in timings]
+    return {
+        "workload": f"gpt-oss-120b 6-turn trajectory, {n} tokens, {CHUNKS} chunked forwards with cache publication",
+        "kept": kept, "copies_per_chunk": ncopies, "occurrences_per_chunk": [t["occurrences"] for t in timings],
+        "host_window_ms": ms("window"), "host_plan_ms": ms("plan"),
+        "advance_ms": ms("advance"), "publish_ms": ms("publish"),
+        "reposition_ms": [round(x, 4) for x in repo],
+        "reposition_pct_hbm_peak": round(100 * alg / (sum(repo) / 1e3) / 1e9 / HBM_PEAK_GBS, 2) if repo else None,
+        "request_wall_ms": round(wall * 1e3, 2),
+        "kernel_launches_per_chunk": {"advance gather": 1, "reposition": 1, "publish gather": 2},
+    }
+
+
 def handoff_config(device, flush):
     """Compacted final-version handoff of the 32k GPT-OSS request: its 19441
     active rows x 36 layers (K and V) packed into a contiguous buffer (P
@@ -582,6 +683,7 @@ def cpu_baseline(pipe, seconds):
     per_token = dt / count
     full_s = compile_s + tables_s + per_token * len(src_all)
     bytes_per_token = 4 * m.n_layers * m.n_heads * m.head_dim * 2
+    chunked_s = _chunked_ownership_port()
     return {
         "value": round(bytes_per_token * count / dt / 1e9, 4),
         "unit": "GB/s",
@@ -592,8 +694,39 @@ def cpu_baseline(pipe, seconds):
                    f"closed form {tables_s * 1e3:.1f} ms on the full request; full-request estimate "
                    f"{full_s * 1e3:.0f} ms"),
         "full_request_ms_estimate": round(full_s * 1e3, 1),
+        "chunked_ownership_ms": round(chunked_s * 1e3, 1),
+        "chunked_ownership_sample": (f"numpy oracle of the chunked-prefill ownership (window, plan, advance, "
+                                     f"publication; {CHUNKS} chunks of the 32768-token trajectory), host time"),
         "host": host_info(),
     }
+
+
+def _chunked_ownership_port():
+    """Host seconds of the numpy oracle over the chunked lifecycle that
+    ``chunked_config`` runs natively (slots stay numpy here)."""
+    from oracle import events as oe
+    from oracle import occurrence as occ
+    from oracle import ownership as own
+
+    n = 32768
+    events, visible = synth.trajectory_events(n, 6, 500, 2000, seed=6)
+    ref = oe.compile_context_layout(*(events[k].numpy() for k in events))
+    visible = visible.numpy()
+    slots = np.random.default_rng(7).permutation(np.arange(1, 3 * n)).astype(np.int64)
+    st = own.State.from_match(np.zeros(0, np.int64), np.zeros(0, np.int32), exact_prefix_len=0)
+    bounds = np.linspace(0, n, CHUNKS + 1).astype(int)
+    used = 0
+    t0 = time.perf_counter()
+    for qs, qe in zip(bounds[:-1], bounds[1:]):
+        win = occ.compile_window(ref, visible, int(qs), int(qe))
+        p = st.plan(win, st.prefill_terminal_keep(ref, int(qe)))
+        q = slots[used : used + qe - qs]
+        extra = slots[used + qe - qs : used + qe - qs + p["extra_page_count"]]
+        used += qe - qs + p["extra_page_count"]
+        st = st.advance(win, p, q, extra, visible).state
+        if qe < n:
+            st = st.publish(st.terminal_slots(), cache_len=int(qe))
+    return time.perf_counter() - t0
 
 
 def host_info():
@@ -753,7 +886,7 @@ def main():
         result["other_configs"] = [tiny_config(device, pipe.flush), ascending_slots_config(device, pipe.flush),
                                    ragged_config(device, pipe.flush), decode_consumer_config(device, pipe.flush),
                                    prefill_config(device, pipe.flush), multistage_config(device, pipe.flush),
-                                   handoff_config(device, pipe.flush)]
+                                   chunked_config(device, pipe.flush), handoff_config(device, pipe.flush)]
         if not args.no_cow:
             print("# copy-on-write configuration ...", file=sys.stderr, flush=True)
             result["other_configs"].append(cow_config(device, pipe.flush))

@@ -420,6 +420,84 @@ int akv_plan_compile(const void* token_ids, int32_t token_ids_dtype,
                      int64_t* drop_event_to_key, uint8_t* effective_repositions,
                      uint8_t* ignored_repositions, int64_t* status);
 
+/*
+ * Host (CPU arrays) ownership plan of one prefill forward over the queries
+ * [query_start, query_end) of a raw prompt of n tokens: which occurrences
+ * of the window need a page (segment keys, this forward's births, published
+ * terminal versions), which reuse an owner row (source_rows[o] = r for the
+ * canonical version of raw r, n + r for its terminal version, -1 unbound),
+ * and the allocated ones in occurrence order with their copy source rows
+ * and (old, new) position pairs.  selected_terminal[query_end]: published
+ * terminal occurrence per raw token or -1.  Outputs sized by the occurrence
+ * count (allocated, copy rows, 2x pairs) and n (cached flags);
+ * *allocated_count receives the allocation count.  Replaces
+ * plan_occurrence_materialization,
+ * akv/system/sglang/srt/context_system/occurrence.py:341-466 (same
+ * decisions and ValueError messages).
+ */
+int akv_plan_ownership(int64_t n, int64_t query_start, int64_t query_end,
+                       int64_t exact_prefix_len, int64_t occurrence_count,
+                       const int32_t* occurrence_raw_tokens,
+                       const int32_t* occurrence_positions,
+                       const int32_t* terminal_occurrences, int64_t key_count,
+                       const int32_t* key_occurrences,
+                       const int32_t* canonical_positions,
+                       const uint8_t* canonical_present,
+                       const uint8_t* canonical_owned,
+                       const uint8_t* terminal_present,
+                       const uint8_t* terminal_keep, int64_t* source_rows,
+                       int64_t* allocated, int64_t* copy_source_rows,
+                       int32_t* copy_position_pairs, int64_t* selected_terminal,
+                       uint8_t* read_cached, uint8_t* repositioned_cached,
+                       int64_t* allocated_count);
+
+/*
+ * Host (CPU arrays) binding of a planned forward: owner rows address the
+ * request's slot sequence old[0:old_count] ++ query[0:query_count] ++
+ * extra[0:extra_count].  Writes the owner row of every occurrence (0 when
+ * unbound), the copy source / destination rows, the successor's owner rows
+ * (ascending) with their ownership and SWA flags, its canonical / terminal
+ * rows and canonical positions over [0, end), the retired private rows
+ * (ascending) and, when track_swa, the fresh copy destinations whose source
+ * has no SWA peer.  counts[3] = {successor rows, retired rows, unused-SWA
+ * rows}; row outputs have capacity old_count + query_count + extra_count.
+ * Replaces the index work of OccurrenceState.advance,
+ * akv/system/sglang/srt/context_system/occurrence.py:632-755.
+ */
+int akv_advance_ownership(
+    int64_t n, int64_t start, int64_t end, int64_t old_count,
+    int64_t query_count, int64_t extra_count, const uint8_t* owned,
+    const int64_t* canonical_rows, const int64_t* terminal_rows,
+    const int32_t* canonical_positions, int32_t track_swa,
+    const uint8_t* swa_resident, int64_t occurrence_count,
+    const int32_t* occurrence_positions, const int32_t* terminal_occurrences,
+    const int64_t* source_rows, const int64_t* allocated,
+    const int64_t* copy_source_rows, const int64_t* selected_terminal,
+    const int32_t* visible_until, int64_t* occurrence_rows,
+    int64_t* copy_source_index, int64_t* copy_destination_index,
+    int64_t* successor_rows, int64_t* retired_rows, int64_t* unused_swa_rows,
+    uint8_t* next_owned, int64_t* next_canonical, int64_t* next_terminal,
+    int32_t* next_positions, uint8_t* next_swa, uint8_t* retired_swa,
+    int64_t* counts);
+
+/*
+ * Batched owner-row -> slot gather (DEVICE arrays).  sources[6 * b ..]:
+ * device address and length of up to three slot pieces of request b
+ * (AKV_I32 or AKV_I64 slots, all of slot_dtype); segment s covers elements
+ * [segment_offsets[s], segment_offsets[s + 1]) and belongs to request
+ * segment_requests[s].  Element i = slot of rows[i] in its request's
+ * concatenated pieces, -1 for row -1; elements [0, wide_count) go to
+ * out_wide (slot_dtype), the rest to out_narrow (int32).  One launch for a
+ * whole batch; replaces the per-request torch.cat and indexing of
+ * akv/system/sglang/srt/context_system/occurrence.py:733-767,795-798,856-864
+ * and the batch concatenation of akv/system/sglang.patch:3174-3180.
+ */
+int akv_gather_slots(int32_t slot_dtype, const int64_t* sources,
+                     int64_t n_segments, const int64_t* segment_offsets,
+                     const int64_t* segment_requests, const int64_t* rows,
+                     int64_t total, int64_t wide_count, void* out_wide,
+                     int32_t* out_narrow, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

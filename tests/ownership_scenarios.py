@@ -319,3 +319,125 @@ class OracleImpl:
 
     def nonterminal_residency(self, st):
         return st.nonterminal_private_residency()
+
+
+def torch_layout(layout):
+    """Oracle layout (numpy) -> the tensor layout the product reads."""
+    import torch
+    from types import SimpleNamespace
+
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32))
+    return SimpleNamespace(
+        birth_positions=i32(layout.birth_positions), birth_stages=i32(layout.birth_stages),
+        transition_offsets=i32(layout.transition_offsets), transition_raw_tokens=i32(layout.transition_raw_tokens),
+        transition_old_positions=i32(layout.transition_old_positions),
+        transition_new_positions=i32(layout.transition_new_positions), positions=i32(layout.positions),
+        keep_mask=torch.from_numpy(np.asarray(layout.keep_mask, dtype=bool).copy()),
+        next_position=int(layout.next_position))
+
+
+class NativeImpl:
+    """``akv_amd.ownership`` (C++ host planner + device gathers) behind the
+    scenario interface; slots live on ``device`` as ``slot_dtype``."""
+
+    def __init__(self, device, slot_dtype=None):
+        import torch
+
+        from akv_amd import occurrence, ownership
+
+        self.torch, self.occ, self.own = torch, occurrence, ownership
+        self.device = device
+        self.dtype = slot_dtype or torch.int64
+        self._layouts = {}
+
+    def _t(self, a, dtype=None, device=None):
+        t = self.torch.from_numpy(np.ascontiguousarray(a).copy())
+        return t.to(dtype or t.dtype).to(device) if device is not None else t.to(dtype or t.dtype)
+
+    def _slots(self, a):
+        return self._t(np.asarray(a, dtype=np.int64), self.dtype, self.device)
+
+    def _bool(self, a):
+        return None if a is None else self._t(np.asarray(a, dtype=bool))
+
+    def _layout(self, layout):
+        if id(layout) not in self._layouts:
+            self._layouts[id(layout)] = (layout, torch_layout(layout))
+        return self._layouts[id(layout)][1]
+
+    @staticmethod
+    def _n(t):
+        return None if t is None else t.detach().cpu().numpy()
+
+    def window(self, layout, visible, qs, qe):
+        lay = self._layout(layout)
+        w = self.occ.compile_occurrence_window(lay, self._t(visible, self.torch.int32), lay.positions,
+                                               query_start=int(qs), query_end=int(qe))
+        return dict(raw=w.occurrence_raw_tokens.numpy(), pos=w.occurrence_positions.numpy(),
+                    birth=w.birth_occurrences.numpy(), terminal=w.terminal_occurrences.numpy(),
+                    keys=w.segment_key_occurrences.numpy(), starts=w.segment_query_starts.numpy(),
+                    ends=w.segment_query_ends.numpy(), key_offsets=w.segment_key_offsets.numpy(), _obj=w)
+
+    def from_match(self, slots, positions, exact, resident, swa):
+        return self.own.OccurrenceState.from_match(
+            self._slots(slots), self._t(positions, self.torch.int32), exact_prefix_len=int(exact),
+            resident=self._bool(resident), swa_resident=self._bool(swa))
+
+    def gap(self, st, slots, positions, resident, end, exact, swa):
+        return st.reuse_match_gap(self._slots(slots), self._t(positions, self.torch.int32), self._bool(resident),
+                                  int(end), exact_prefix_len=int(exact), swa_resident=self._bool(swa))
+
+    def keep(self, st, layout, qe):
+        return st.prefill_terminal_keep(self._layout(layout), int(qe)).numpy()
+
+    @staticmethod
+    def _plan_dict(p):
+        return dict(source_rows=p.source_rows.numpy(), allocated=p.allocated_occurrences.numpy(),
+                    copy_source_rows=p.copy_source_rows.numpy(), pairs=p.copy_position_pairs.numpy(),
+                    terminal_occurrences=p.terminal_occurrences.numpy(), read_cached=p.read_cached.numpy(),
+                    repositioned_cached=p.repositioned_cached.numpy(), extra_page_count=p.extra_page_count, _obj=p)
+
+    def plan(self, st, win, keep):
+        return self._plan_dict(st.plan(win["_obj"], self._bool(keep)))
+
+    def plan_free(self, win, cpos, present, owned, tpresent, keep, qs, qe, exact):
+        return self._plan_dict(self.own.plan_occurrence_materialization(
+            win["_obj"], self._t(cpos, self.torch.int32), self._bool(present), self._bool(owned),
+            self._bool(tpresent), self._bool(keep), query_start=int(qs), query_end=int(qe),
+            exact_prefix_len=int(exact)))
+
+    def advance(self, st, win, p, q_slots, extra, visible):
+        a = st.advance(win["_obj"], p["_obj"], self._slots(q_slots), self._slots(extra),
+                       self._t(visible, self.torch.int32))
+        n = self._n
+        return a.state, dict(occurrence_slots=n(a.occurrence_slots), copy_source_slots=n(a.copy_source_slots),
+                             copy_destination_slots=n(a.copy_destination_slots),
+                             copy_position_pairs=n(a.copy_position_pairs), retired_slots=n(a.retired_slots),
+                             unused_swa_slots=n(a.unused_swa_slots), retired_swa_resident=n(a.retired_swa_resident))
+
+    def fields(self, st):
+        n = self._n
+        return dict(slots=n(st.slots), owned=n(st.owned), canonical_rows=n(st.canonical_rows),
+                    terminal_rows=n(st.terminal_rows), canonical_positions=n(st.canonical_positions),
+                    exact_prefix_len=np.int64(st.exact_prefix_len), swa_resident=n(st.swa_resident))
+
+    def terminal_slots(self, st):
+        return self._n(st.terminal_slots())
+
+    def terminal_swa(self, st):
+        return self._n(st.terminal_swa_residency())
+
+    def publish(self, st, matched, cache_len, swa):
+        return st.publish(self._slots(matched), cache_len=cache_len, swa_resident=self._bool(swa))
+
+    def drop(self, st, mask):
+        return st.drop_borrowed_raw(self._bool(mask))
+
+    def private(self, st):
+        return self._n(st.private_slots())
+
+    def nonterminal(self, st):
+        return self._n(st.nonterminal_private_slots())
+
+    def nonterminal_residency(self, st):
+        return self._n(st.nonterminal_private_residency())

@@ -69,6 +69,18 @@ def test_validation_rejects_before_any_device_work(lib):
     assert lib.akv_decode_indices(*zeros(lib.akv_decode_indices)) == 0
     assert lib.akv_decode_indices(*zeros(lib.akv_decode_indices, a16=3)) == _lib.AKV_EINVAL
     assert lib.akv_build_indptr(None, 0, 3, None, 0, None, 1, 1, None) == _lib.AKV_EINVAL
+    assert lib.akv_gather_slots(*zeros(lib.akv_gather_slots, a0=7)) == _lib.AKV_EINVAL
+    assert "slot dtype" in _lib.last_error()
+    assert lib.akv_gather_slots(*zeros(lib.akv_gather_slots)) == 0  # nothing to gather
+    assert lib.akv_gather_slots(*zeros(lib.akv_gather_slots, a6=5, a7=9)) == _lib.AKV_EINVAL
+    assert lib.akv_gather_slots(*zeros(lib.akv_gather_slots, a6=5, a7=5)) == _lib.AKV_EINVAL
+    assert "null pointer" in _lib.last_error()
+    assert lib.akv_plan_ownership(*zeros(lib.akv_plan_ownership, a0=4, a1=2, a2=1)) == _lib.AKV_EINVAL
+    assert "Invalid occurrence ownership/query boundaries" in _lib.last_error()
+    assert lib.akv_plan_ownership(*zeros(lib.akv_plan_ownership, a0=4, a1=0, a2=4, a4=4)) == _lib.AKV_EINVAL
+    assert "null host pointer" in _lib.last_error()
+    assert lib.akv_advance_ownership(*zeros(lib.akv_advance_ownership, a0=4, a1=0, a2=4, a4=3, a12=4)) == _lib.AKV_EINVAL
+    assert "Context admission does not cover the selected window" in _lib.last_error()
 
 
 def _events(n, drops, repos):

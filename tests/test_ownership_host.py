@@ -1,0 +1,119 @@
+"""Host ownership planner (C++: ``akv_plan_ownership`` /
+``akv_advance_ownership``) and the Python mirror of ``OccurrenceState``
+against the golden traces of the reference module, on the CPU.
+
+The device gather (``akv_gather_slots``) is replaced here by a numpy
+statement of its contract -- element i = slot of rows[i] in its request's
+concatenated pieces, -1 for row -1 -- so every host decision, segment and
+state transition is checked without a GPU; ``tests/test_gpu_ownership.py``
+runs the same traces through the HIP kernel."""
+
+import numpy as np
+import pytest
+import torch
+
+import ownership_scenarios as scenarios
+from akv_amd import ownership
+from golden import make_ownership_vectors as vectors
+
+
+def _gather_on_cpu(self, extra_i32=()):
+    pieces = [np.concatenate([p.numpy().astype(np.int64) for p in req if p is not None] or [np.zeros(0, np.int64)])
+              for req in self.requests]
+
+    def resolve(b, rows):
+        out = np.full(len(rows), -1, dtype=np.int64)
+        ok = rows >= 0
+        assert np.all(rows[ok] < len(pieces[b])), "owner row beyond the request's slots"
+        out[ok] = pieces[b][rows[ok]]
+        return out
+
+    wide = [torch.from_numpy(resolve(b, r)).to(self.dtype) for b, r in self.wide]
+    narrow = [torch.from_numpy(resolve(b, r).astype(np.int32)) for b, r in self.narrow]
+    extra = [torch.from_numpy(np.ascontiguousarray(e, dtype=np.int32).reshape(-1)) for e in extra_i32]
+    return wide, narrow, extra
+
+
+@pytest.fixture
+def cpu_gather(monkeypatch):
+    monkeypatch.setattr(ownership._Gather, "run", _gather_on_cpu)
+
+
+def _same(a, b):
+    if a is None or b is None:
+        return a is None and b is None
+    a, b = np.asarray(a), np.asarray(b)
+    return a.shape == b.shape and np.array_equal(a.astype(np.int64), b.astype(np.int64))
+
+
+@pytest.mark.parametrize("slot_dtype", [torch.int64, torch.int32])
+def test_lifecycles_match_reference_traces(cpu_gather, slot_dtype):
+    golden = vectors.unpack(np.load(vectors.OUT))
+    impl = scenarios.NativeImpl(torch.device("cpu"), slot_dtype)
+    for seed in vectors.SEEDS:
+        want = golden[seed]
+        got = scenarios.run(scenarios.make(seed), impl)
+        assert [k for k, _ in got] == [k for k, _ in want], seed
+        for (name, a), (_, b) in zip(got, want):
+            assert _same(a, b), (seed, name)
+
+
+def test_direct_plans_match_reference(cpu_gather):
+    golden = vectors.unpack(np.load(vectors.OUT))
+    impl = scenarios.NativeImpl(torch.device("cpu"))
+    for seed in vectors.SEEDS:
+        got = scenarios.run_plan_case(scenarios.plan_case(seed), impl)
+        want = golden[vectors.PLAN_CASES + seed]
+        assert [k for k, _ in got] == [k for k, _ in want], seed
+        for (name, a), (_, b) in zip(got, want):
+            assert _same(a, b), (seed, name)
+
+
+def test_reference_messages(cpu_gather):
+    impl = scenarios.NativeImpl(torch.device("cpu"))
+    sc = scenarios.make(3)
+    lay = scenarios.torch_layout(sc["layout"])
+    n = sc["n"]
+    win = impl.window(sc["layout"], sc["visible"], 2, n)["_obj"]
+    z = torch.zeros(2, dtype=torch.bool)
+    pos = lay.positions[:2].clone()
+    keep = torch.ones(n, dtype=torch.bool)
+    with pytest.raises(ValueError, match="Invalid occurrence ownership/query boundaries"):
+        ownership.plan_occurrence_materialization(win, pos, z, z, z, keep, query_start=2, query_end=n,
+                                                  exact_prefix_len=3)
+    with pytest.raises(ValueError, match="aligned CPU metadata"):
+        ownership.plan_occurrence_materialization(win, pos.long(), z, z, z, keep, query_start=2, query_end=n,
+                                                  exact_prefix_len=0)
+    with pytest.raises(ValueError, match="does not cover the planned queries"):
+        ownership.plan_occurrence_materialization(win, pos, z, z, z, keep[:-1], query_start=2, query_end=n - 1,
+                                                  exact_prefix_len=0)
+    with pytest.raises(ValueError, match="Invalid Context match ownership metadata"):
+        ownership.OccurrenceState.from_match(torch.zeros(3, dtype=torch.int64), torch.zeros(2, dtype=torch.int32),
+                                             exact_prefix_len=0)
+    st = ownership.OccurrenceState.from_match(torch.arange(2), lay.positions[:2].clone(), exact_prefix_len=2)
+    p = st.plan(win, st.prefill_terminal_keep(lay, n))
+    with pytest.raises(ValueError, match="Context admission does not cover the selected window"):
+        st.advance(win, p, torch.arange(n - 3), torch.arange(p.extra_page_count), torch.from_numpy(sc["visible"]))
+    with pytest.raises(ValueError, match="Distinct raw tokens|must cover the raw terminal table"):
+        st.publish(torch.zeros(5, dtype=torch.int64))
+    with pytest.raises(ValueError, match="Drop ownership mask"):
+        st.drop_borrowed_raw(torch.zeros(7, dtype=torch.bool))
+
+
+def test_free_context_slots_splits_by_swa_residency(cpu_gather):
+    class Alloc:
+        def __init__(self):
+            self.calls = []
+
+        def free(self, s):
+            self.calls.append(("free", s.tolist()))
+
+        def free_full(self, s):
+            self.calls.append(("free_full", s.tolist()))
+
+    a = Alloc()
+    slots = torch.tensor([5, 6, 7, 8])
+    ownership.free_context_slots(a, slots, torch.tensor([True, False, True, False]))
+    ownership.free_context_slots(a, slots, None)
+    ownership.free_context_slots(a, slots, torch.zeros(4, dtype=torch.bool))
+    assert a.calls == [("free", [5, 7]), ("free_full", [6, 8]), ("free", [5, 6, 7, 8]), ("free_full", [5, 6, 7, 8])]
