@@ -201,74 +201,3 @@ class ContextLayerCopy:
             skip_unmapped=self.skip_unmapped,
             rotary_dim=self.rotary_dim,
         )
-
-
-@dataclass(frozen=True)
-class PoolLayer:
-    """One attention layer's KV buffers and RoPE binding (``ContextPoolLayer``)."""
-
-    layer_id: int
-    sliding_window: bool
-    k_buffer: torch.Tensor
-    v_buffer: torch.Tensor
-    cos_sin_cache: torch.Tensor
-    is_neox_style: bool
-    rotary_dim: int
-
-
-class LayerGroups:
-    """Groups compatible layers so one launch repositions all of them.
-
-    Mirrors ``ContextModelBinding.reposition_existing``
-    (``akv/system/sglang/srt/layers/attention/context_backend.py:432-472``):
-    layers that share (window kind, shape, strides, dtype, RoPE table, style,
-    rotary width) go into one pointer table, built once on the device.
-    ``swa_translate`` maps full-attention slots to a separate SWA pool's slots
-    (``None`` when SWA layers share the full pool).
-    """
-
-    def __init__(self, layers):
-        groups = {}
-        for layer in layers:
-            key = (
-                layer.sliding_window,
-                tuple(layer.k_buffer.shape),
-                layer.k_buffer.stride(),
-                layer.v_buffer.stride(),
-                layer.k_buffer.dtype,
-                layer.cos_sin_cache.data_ptr(),
-                layer.is_neox_style,
-                layer.rotary_dim,
-            )
-            groups.setdefault(key, []).append(layer)
-        self.groups = []
-        for items in groups.values():
-            device = items[0].k_buffer.device
-            k_ptrs = torch.tensor([x.k_buffer.data_ptr() for x in items], dtype=torch.uint64).to(device)
-            v_ptrs = torch.tensor([x.v_buffer.data_ptr() for x in items], dtype=torch.uint64).to(device)
-            self.groups.append((items[0], k_ptrs, v_ptrs))
-
-    @property
-    def launches(self):
-        return len(self.groups)
-
-    def reposition_existing(self, source, destination, positions, swa_translate=None):
-        for layer, k_ptrs, v_ptrs in self.groups:
-            src, dst, separate_swa = source, destination, False
-            if layer.sliding_window and swa_translate is not None:
-                separate_swa = True
-                src = swa_translate(source).to(torch.int32)
-                dst = swa_translate(destination).to(torch.int32)
-            reposition_kv_layers(
-                k_ptrs,
-                v_ptrs,
-                layer.k_buffer,
-                layer.v_buffer,
-                src,
-                dst,
-                positions,
-                layer.cos_sin_cache,
-                is_neox_style=layer.is_neox_style,
-                rotary_dim=layer.rotary_dim,
-                skip_unmapped=separate_swa,
-            )
