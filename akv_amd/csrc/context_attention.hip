@@ -80,6 +80,24 @@ struct CtxArgs {
   int32_t group, tokens_per_block;
 };
 
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Maximum over the four lanes col, col+16, col+32, col+48 of each 16-lane
+// column group, on the VALU: v_permlane16_swap / v_permlane32_swap exchange
+// rows of 16 (32) lanes, so max(swapped pair) = max(own, partner).
+__device__ __forceinline__ float row_max(float x) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, x);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  // copy the pair out before the bit casts: a bit cast of a vector element
+  // reference reads element 0
+  const uint32_t a0 = r16[0], a1 = r16[1];
+  x = fmaxf(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
+  const uint32_t c = __builtin_bit_cast(uint32_t, x);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  const uint32_t c0 = r32[0], c1 = r32[1];
+  return fmaxf(__builtin_bit_cast(float, c0), __builtin_bit_cast(float, c1));
+}
+
 __device__ __forceinline__ u32x4 load16(const __bf16* p) {
   return *((const global_u32x4*)p);
 }
@@ -313,62 +331,61 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
     // online softmax per row (column of S^T: lanes col, col+16, col+32, col+48),
     // log2 domain.  The reference maximum m_run moves only when a tile's
     // maximum exceeds it by more than kLazy, so most tiles skip rescaling
-    // O and l; p = 2^(t - m_run) then stays below 2^kLazy.
+    // O and l; p = 2^(t - m_run) then stays below 2^kLazy.  Masked scores
+    // become -inf in place (exp2 -> 0): no per-key branches, one shared
+    // softmax, and tiles wholly inside every row's range skip the mask.
     bf16x8 pop[2][2];
+    {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      float raw[4][4];
-      bool vis[4][4];
-      float mx = -INFINITY;
-      if (masked) {
-        // causal: key index <= the row's token; window: key pos >= row pos - W
-        const int32_t climit = ext ? t0 + row_tl[s] - base : kKeys;
-        const int32_t last = climit < count - 1 ? climit : count - 1;
-        const int32_t thr = a.window >= 0 ? row_rel[s] - a.window : -kFar - 1;
+      for (int s = 0; s < 2; ++s) {
+        f32x4 t[4];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt) t[kt] = sacc[kt][s];
+        if (masked) {
+          // causal: key index <= the row's token; window: key pos >= row pos - W
+          const int32_t climit = ext ? t0 + row_tl[s] - base : kKeys;
+          const int32_t last = climit < count - 1 ? climit : count - 1;
+          const int32_t thr = a.window >= 0 ? row_rel[s] - a.window : -kFar - 1;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = 16 * kt + 4 * quad + i;
-            vis[kt][i] = key <= last && sm.pos[buf][key] >= thr;
-            raw[kt][i] = sacc[kt][s][i];
-            if (vis[kt][i]) mx = fmaxf(mx, raw[kt][i]);
+          for (int kt = 0; kt < 4; ++kt) {
+            const i32x4 kp = *reinterpret_cast<const i32x4*>(&sm.pos[buf][16 * kt + 4 * quad]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const bool vis = (16 * kt + 4 * quad + i <= last) & (kp[i] >= thr);
+              t[kt][i] = vis ? t[kt][i] : -INFINITY;
+            }
           }
-      } else {
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            vis[kt][i] = true;
-            raw[kt][i] = sacc[kt][s][i];
-            mx = fmaxf(mx, raw[kt][i]);
-          }
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float tmax = mx * a.scale_log2;  // -inf when the row sees nothing here
-      const bool bump = tmax > m_run[s] + kLazy;
-      if (__builtin_amdgcn_ballot_w64(bump)) {
-        const float m_new = bump ? tmax : m_run[s];
-        const float alpha = bump ? __builtin_amdgcn_exp2f(m_run[s] - m_new) : 1.f;  // m_run = -inf -> 0
-        lacc[s] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] *= alpha;
-        m_run[s] = m_new;
-      }
-      const float neg_m = -m_run[s];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          raw[kt][i] = vis[kt][i] ? __builtin_amdgcn_exp2f(fmaf(raw[kt][i], a.scale_log2, neg_m)) : 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pop[s][kk][i] = static_cast<__bf16>(raw[2 * kk][i]);
-          pop[s][kk][4 + i] = static_cast<__bf16>(raw[2 * kk + 1][i]);
         }
+        float mx = fmaxf(fmaxf(fmaxf(t[0][0], t[0][1]), fmaxf(t[0][2], t[0][3])),
+                         fmaxf(fmaxf(t[1][0], t[1][1]), fmaxf(t[1][2], t[1][3])));
+        mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(t[2][0], t[2][1]), fmaxf(t[2][2], t[2][3])),
+                             fmaxf(fmaxf(t[3][0], t[3][1]), fmaxf(t[3][2], t[3][3]))));
+        mx = row_max(mx);
+        const float tmax = mx * a.scale_log2;  // -inf when the row sees nothing here
+        const bool bump = tmax > m_run[s] + kLazy;
+        if (__builtin_amdgcn_ballot_w64(bump)) {
+          const float m_new = bump ? tmax : m_run[s];
+          const float alpha = bump ? __builtin_amdgcn_exp2f(m_run[s] - m_new) : 1.f;  // m_run = -inf -> 0
+          lacc[s] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] *= alpha;
+          m_run[s] = m_new;
+        }
+        // a row that has seen no key yet has only -inf scores: any finite shift
+        const float neg_m = m_run[s] == -INFINITY ? 0.f : -m_run[s];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          f32x4 e0, e1;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            e0[i] = __builtin_amdgcn_exp2f(fmaf(t[2 * kk][i], a.scale_log2, neg_m));
+            e1[i] = __builtin_amdgcn_exp2f(fmaf(t[2 * kk + 1][i], a.scale_log2, neg_m));
+          }
+          const bf16x4 b0 = __builtin_convertvector(e0, bf16x4);
+          const bf16x4 b1 = __builtin_convertvector(e1, bf16x4);
+          pop[s][kk] = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+      }
     }
 
     // O^T += V^T . P^T
@@ -500,6 +517,9 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
   if (bases & 15) return fail(AKV_EINVAL, "akv_context_attention: tensors must be 16-byte aligned");
   if (n_segments > 65535 || kv_heads > 65535)
     return fail(AKV_EINVAL, "akv_context_attention: batch too large");
+  // masked scores are -inf before the scale: the softmax needs scale > 0
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(AKV_EINVAL, "akv_context_attention: scale must be positive and finite");
   CtxArgs a{};
   a.q = static_cast<const __bf16*>(q);
   a.k_ext = static_cast<const __bf16*>(k_ext);

@@ -129,3 +129,17 @@ def test_metadata_path_ordinary_sequences(device):
     want = oat.context_attention(_f32(q), _f32(ke), _f32(ve), _f32(pool_k), _f32(pool_v), qo, kv,
                                  slots.cpu().numpy()[occ], d ** -0.5, q_positions=qpos, kv_positions=kpos)
     assert np.abs(_f32(out) - want).max() <= TOL
+
+
+def test_rejects_nonpositive_scale(device):
+    """Masked scores are -inf before scaling, so the scale must be positive."""
+    c = _case(device, 16, 2, 64, [5], [3], seed=4)
+    dv = c["dev"]
+    out = torch.empty(dv["q"].shape, dtype=torch.float32, device=device)
+    qo = torch.from_numpy(c["qo"]).to(device)
+    kv = torch.from_numpy(c["kv"]).to(device)
+    idx = torch.from_numpy(c["idx"]).to(device)
+    for scale in (0.0, -0.125, float("nan")):
+        with pytest.raises(ValueError, match="scale must be positive"):
+            ca.extend_attention_fwd(dv["q"], dv["ke"], dv["ve"], out, dv["kp"], dv["vp"], qo, kv, idx, None, True,
+                                    None, 5, sm_scale=scale)
