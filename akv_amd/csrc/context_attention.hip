@@ -85,20 +85,39 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 // Maximum over the four lanes col, col+16, col+32, col+48 of each 16-lane
 // column group, on the VALU: v_permlane16_swap / v_permlane32_swap exchange
 // rows of 16 (32) lanes, so max(swapped pair) = max(own, partner).
+// v_max3_f32 / v_max_f32 without the canonicalising moves the compiler adds
+// around fmaxf of matrix-core results.  Only the softmax's range uses these
+// maxima: a NaN score still reaches the output through exp2 and the MFMAs.
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+__device__ __forceinline__ float max2(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 __device__ __forceinline__ float row_max(float x) {
   const uint32_t b = __builtin_bit_cast(uint32_t, x);
   const auto r16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
   // copy the pair out before the bit casts: a bit cast of a vector element
   // reference reads element 0
   const uint32_t a0 = r16[0], a1 = r16[1];
-  x = fmaxf(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
+  x = max2(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
   const uint32_t c = __builtin_bit_cast(uint32_t, x);
   const auto r32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
   const uint32_t c0 = r32[0], c1 = r32[1];
-  return fmaxf(__builtin_bit_cast(float, c0), __builtin_bit_cast(float, c1));
+  return max2(__builtin_bit_cast(float, c0), __builtin_bit_cast(float, c1));
 }
 
 __device__ __forceinline__ u32x4 load16(const __bf16* p) {
+  return *((const global_u32x4*)p);
+}
+
+__device__ __forceinline__ u32x4 load16b(const char* p) {
   return *((const global_u32x4*)p);
 }
 
@@ -150,6 +169,12 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
   const __bf16* vext = a.v_ext + qo0 * a.ve_st + g * a.ve_sh;
   const __bf16* kpool = a.k_pool + g * a.kp_sh;
   const __bf16* vpool = a.v_pool + g * a.vp_sh;
+  const char* kext_b = reinterpret_cast<const char*>(kext);
+  const char* vext_b = reinterpret_cast<const char*>(vext);
+  const char* kpool_b = reinterpret_cast<const char*>(kpool);
+  const char* vpool_b = reinterpret_cast<const char*>(vpool);
+  const uint64_t ke_sb = 2u * static_cast<uint32_t>(a.ke_st), ve_sb = 2u * static_cast<uint32_t>(a.ve_st);
+  const uint64_t kp_sb = 2u * static_cast<uint32_t>(a.kp_ss), vp_sb = 2u * static_cast<uint32_t>(a.vp_ss);
   auto qpos_of = [&](int32_t i) -> int64_t {  // position of query i of the segment
     if constexpr (POS) return static_cast<int64_t>(qpos[i]);
     return static_cast<int64_t>(plen) + i;
@@ -231,6 +256,8 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
     // branch-free: keys past the end read the last valid row (masked out later)
     const bool ext = it >= n_pref;
     const int32_t base = tile_base(it);
+    // addresses: one 32 x 32 -> 64-bit multiply-add each (row index and byte
+    // stride fit 32 bits: the host bounds strides to 31 bits of elements)
     if (ext) {
 #pragma unroll
       for (int u = 0; u < kRounds; ++u) {
@@ -240,9 +267,9 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const int32_t j = base + 2 * p + e;
-          const int64_t off = static_cast<int64_t>(j < e_hi ? j : e_hi - 1);
-          kreg[u][e] = load16(kext + off * a.ke_st + 8 * cc);
-          vreg[u][e] = load16(vext + off * a.ve_st + 8 * cc);
+          const uint64_t off = static_cast<uint32_t>(j < e_hi ? j : e_hi - 1);
+          kreg[u][e] = load16b(kext_b + 16 * cc + off * ke_sb);
+          vreg[u][e] = load16b(vext_b + 16 * cc + off * ve_sb);
         }
       }
     } else {
@@ -253,8 +280,14 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
         const int cc = c - p * kChunks;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          kreg[u][e] = load16(kpool + slot[u][e] * a.kp_ss + 8 * cc);
-          vreg[u][e] = load16(vpool + slot[u][e] * a.vp_ss + 8 * cc);
+          if constexpr (sizeof(IdxT) == 4) {
+            const uint64_t so = static_cast<uint32_t>(slot[u][e]);
+            kreg[u][e] = load16b(kpool_b + 16 * cc + so * kp_sb);
+            vreg[u][e] = load16b(vpool_b + 16 * cc + so * vp_sb);
+          } else {
+            kreg[u][e] = load16(kpool + slot[u][e] * a.kp_ss + 8 * cc);
+            vreg[u][e] = load16(vpool + slot[u][e] * a.vp_ss + 8 * cc);
+          }
         }
       }
     }
@@ -356,10 +389,13 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
             }
           }
         }
-        float mx = fmaxf(fmaxf(fmaxf(t[0][0], t[0][1]), fmaxf(t[0][2], t[0][3])),
-                         fmaxf(fmaxf(t[1][0], t[1][1]), fmaxf(t[1][2], t[1][3])));
-        mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(t[2][0], t[2][1]), fmaxf(t[2][2], t[2][3])),
-                             fmaxf(fmaxf(t[3][0], t[3][1]), fmaxf(t[3][2], t[3][3]))));
+        // 16 values in 8 three-input maxima
+        const float m0 = max3(t[0][0], t[0][1], t[0][2]);
+        const float m1 = max3(t[0][3], t[1][0], t[1][1]);
+        const float m2 = max3(t[1][2], t[1][3], t[2][0]);
+        const float m3 = max3(t[2][1], t[2][2], t[2][3]);
+        const float m4 = max3(t[3][0], t[3][1], t[3][2]);
+        float mx = max3(max3(m0, m1, m2), max3(m3, m4, t[3][3]), -INFINITY);
         mx = row_max(mx);
         const float tmax = mx * a.scale_log2;  // -inf when the row sees nothing here
         const bool bump = tmax > m_run[s] + kLazy;
