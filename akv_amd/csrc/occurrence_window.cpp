@@ -4,7 +4,8 @@
 // Same results and error messages as compile_occurrence_window
 // (akv/system/sglang/srt/context_system/occurrence.py:112-265), in C++ behind
 // the C ABI.  One replay routine drives the count and the fill entry points
-// through a sink, so both passes agree.
+// through a sink, so both passes agree; the fill checks every write against
+// the caller's counts.
 //
 // Replay: every raw token starts as its birth occurrence (id = raw index) at
 // its birth position.  Stages are walked in order; a stage first applies its
@@ -58,19 +59,29 @@ struct Sink {
   int32_t* key_offsets = nullptr;
   int32_t* key_occ = nullptr;
 
+  // fill mode: capacities of the caller's arrays; every write is checked
+  int64_t cap_occurrences = 0, cap_segments = 0, cap_keys = 0;
+  static void overflow() {
+    throw std::invalid_argument("akv_window_compile: output capacities do not match the window");
+  }
   void occurrence(int32_t raw, int32_t pos) {
     if (fill) {
+      if (occurrences >= cap_occurrences) overflow();
       occ_raw[occurrences] = raw;
       occ_pos[occurrences] = pos;
     }
     ++occurrences;
   }
   void key(int32_t id) {
-    if (fill) key_occ[keys] = id;
+    if (fill) {
+      if (keys >= cap_keys) overflow();
+      key_occ[keys] = id;
+    }
     ++keys;
   }
   void segment(int32_t start, int32_t end) {
     if (fill) {
+      if (segments >= cap_segments) overflow();
       seg_start[segments] = start;
       seg_end[segments] = end;
       key_offsets[segments + 1] = static_cast<int32_t>(keys);
@@ -233,14 +244,13 @@ extern "C" int akv_window_compile(int64_t n, const int32_t* birth_positions, con
   Inputs in{n, birth_positions, birth_stages, transition_offsets, stage_count, transition_raw_tokens,
             transition_old_positions, transition_new_positions, visible_until, terminal_positions,
             query_start, query_end};
-  // count first: the fill pass writes exactly the counted sizes
-  Sink probe;
-  int rc = run(in, probe);
-  if (rc) return rc;
-  if (probe.occurrences != counts[0] || probe.segments != counts[1] || probe.keys != counts[2])
-    return fail(AKV_EINVAL, "akv_window_compile: output capacities do not match the window");
+  // one replay: every write is bounded by the caller's counts, and the
+  // counts must come out exact
   Sink sink;
   sink.fill = true;
+  sink.cap_occurrences = counts[0];
+  sink.cap_segments = counts[1];
+  sink.cap_keys = counts[2];
   sink.occ_raw = occurrence_raw_tokens;
   sink.occ_pos = occurrence_positions;
   sink.terminal_occ = terminal_occurrences;
@@ -248,6 +258,11 @@ extern "C" int akv_window_compile(int64_t n, const int32_t* birth_positions, con
   sink.seg_end = segment_query_ends;
   sink.key_offsets = segment_key_offsets;
   sink.key_occ = segment_key_occurrences;
+  if (counts[1] < 0) return fail(AKV_EINVAL, "akv_window_compile: output capacities do not match the window");
   segment_key_offsets[0] = 0;
-  return run(in, sink);
+  const int rc = run(in, sink);
+  if (rc) return rc;
+  if (sink.occurrences != counts[0] || sink.segments != counts[1] || sink.keys != counts[2])
+    return fail(AKV_EINVAL, "akv_window_compile: output capacities do not match the window");
+  return AKV_OK;
 }
