@@ -21,15 +21,7 @@ import torch
 
 from .context_attention import ContextAttentionMetadata, ContextAttentionPlan, ContextSequence
 from .ops import ContextLayerCopy, reposition_kv_layers
-
-
-def request_row(pool, index):
-    """The request's token row, or its side row when it overflowed
-    (``akv/system/sglang/srt/context_system/request_storage.py:240-244``)."""
-    rows = getattr(pool, "_context_rows", None)
-    if rows and index in rows:
-        return rows[index]
-    return pool.req_to_token[index]
+from .request_rows import request_row
 
 
 @dataclass(frozen=True)

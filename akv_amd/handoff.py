@@ -23,7 +23,8 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
-from .binding import ContextModelBinding, request_row
+from .binding import ContextModelBinding
+from .request_rows import request_row
 from .ownership import OccurrenceState, _Gather
 from .page_table import ContextDecodeLayout
 
