@@ -16,15 +16,17 @@
 // context window are ordered), which lets a workgroup start the prefix and
 // extend loops at the first key inside the window.
 //
-// Workgroup = (block of 128 / G query tokens, KV head g, segment), with the
-// G q heads of the group packed as rows: row r = token * G + head, 128 rows,
-// 4 waves x 32 rows.  Per 64-key tile (K and V key-major in LDS, double
-// buffered, the next tile's global loads -- and the slots of the tile after
-// it -- in flight during this tile's math):
-//   S^T[64 keys x 32 rows] = K . Q^T          v_mfma_f32_16x16x32_bf16
+// Workgroup = (block of R / G query tokens, KV head g, segment), with the
+// G q heads of the group packed as rows: row r = token * G + head; R = 256
+// rows at head_dim 64 (4 waves x 64 rows, so each wave's reads of a K/V tile
+// from LDS feed 64 rows), 128 at head_dim 128 (4 waves x 32 rows).  Per
+// 64-key tile (K and V key-major in LDS, double buffered, the next tile's
+// global loads -- and the slots of the tile after it -- in flight during
+// this tile's math), for a wave's W rows:
+//   S^T[64 keys x W rows] = K . Q^T           v_mfma_f32_16x16x32_bf16
 //   online softmax per row (column of S^T) in the exp2 domain, the running
 //   maximum moving only when a tile exceeds it by 2^8 (lazy rescale)
-//   O^T[D x 32 rows] += V^T . P^T             v_mfma_f32_16x16x32_bf16
+//   O^T[D x W rows] += V^T . P^T              v_mfma_f32_16x16x32_bf16
 //   l[rows] += 1^T . P^T                      (row sums of the same bf16 P)
 // P^T leaves the first MFMA in the B-operand layout of the second (any
 // consistent split of the 32-long k axis over lanes gives the same product:
@@ -37,6 +39,7 @@
 // D[4(l/16)+i][l%16]; ds_read_b64_tr_b16 -- within each 16-lane group, lane
 // j receives element j%4 of the 8-byte rows read by lanes j/4 + 4i, i < 4.
 #include <cmath>
+#include <type_traits>
 
 #include "common.h"
 
@@ -52,7 +55,10 @@ typedef __attribute__((address_space(1))) u32x4 global_u32x4;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-constexpr int kRows = 128;  // (token, head) rows per workgroup
+// 16-row subtiles per wave: 4 at head_dim 64 (each wave's K/V tile reads
+// from LDS feed 64 rows), 2 at head_dim 128 (register budget)
+constexpr int sub_tiles(int d) { return d == 64 ? 4 : 2; }
+constexpr int rows_per_block(int d) { return 4 * 16 * sub_tiles(d); }  // (token, head) rows
 constexpr int kThreads = 256;
 constexpr int kKeys = 64;  // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
@@ -136,7 +142,8 @@ __device__ __forceinline__ int32_t rel_pos(int64_t p, int64_t base) {
 }
 
 template <int D, typename IdxT, typename PosT, bool POS>
-__global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_kernel(const CtxArgs a) {
+__global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const CtxArgs a) {
+  constexpr int kSub = sub_tiles(D);
   constexpr int kChunks = D / 8;               // 16 B chunks per key row
   constexpr int kRounds = kChunks / 8;         // (key pair, chunk) items per thread
   constexpr int kKSteps = D / 32;              // MFMA k-steps over head dims
@@ -211,31 +218,32 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
     return it < n_pref ? p_lo + it * kKeys : e_lo + (it - n_pref) * kKeys;
   };
 
-  // this lane's rows: row subtile s covers rows wave*32 + 16s + col
-  int32_t row_tl[2], row_rel[2];  // token within the block, position relative to qbase
-  int row_head[2];
-  bool row_ok[2];
-  bf16x8 qop[2][kKSteps];
+  // this lane's rows: row subtile s covers rows wave * 16 kSub + 16s + col
+  // per row subtile: (token within the block) | (q head << 16), and the
+  // row's position relative to qbase
+  int32_t row_th[kSub], row_rel[kSub];
+  bf16x8 qop[kSub][kKSteps];
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int r = wave * 32 + 16 * s + col;
+  for (int s = 0; s < kSub; ++s) {
+    const int r = wave * (16 * kSub) + 16 * s + col;
     const int tl = r / G;
-    row_tl[s] = tl;
-    row_head[s] = g * G + (r - tl * G);
-    row_ok[s] = t0 + tl < qlen;
-    row_rel[s] = row_ok[s] ? rel_pos(qpos_of(t0 + tl), qbase) : last_rel;
+    const int head = g * G + (r - tl * G);
+    row_th[s] = tl | (head << 16);
+    const bool ok = t0 + tl < qlen;
+    row_rel[s] = ok ? rel_pos(qpos_of(t0 + tl), qbase) : last_rel;
 #pragma unroll
     for (int ks = 0; ks < kKSteps; ++ks) {
       u32x4 w = {0u, 0u, 0u, 0u};
-      if (row_ok[s])
-        w = load16(a.q + (qo0 + t0 + tl) * a.q_st + static_cast<int64_t>(row_head[s]) * a.q_sh + 32 * ks + 8 * quad);
+      if (ok)
+        w = load16(a.q + (qo0 + t0 + tl) * a.q_st + static_cast<int64_t>(head) * a.q_sh + 32 * ks + 8 * quad);
       qop[s][ks] = __builtin_bit_cast(bf16x8, w);
     }
   }
 
   // tile staging: thread item u = key pair p (keys 2p, 2p+1) x 16 B chunk cc,
   // for K and V.  Prefix slots are fetched one tile ahead of their rows.
-  int64_t slot[kRounds][2];
+  using SlotT = typename std::conditional<sizeof(IdxT) == 4, uint32_t, int64_t>::type;
+  SlotT slot[kRounds][2];
   u32x4 kreg[kRounds][2], vreg[kRounds][2];
   int64_t preg = 0;  // raw position of key tid of the staged tile
   bool pvalid = false;
@@ -248,7 +256,7 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int32_t j = base + 2 * p + e;
-        slot[u][e] = static_cast<int64_t>(slots[j < plen ? j : plen - 1]);
+        slot[u][e] = static_cast<SlotT>(slots[j < plen ? j : plen - 1]);
       }
     }
   };
@@ -314,13 +322,17 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
     if (tid < kKeys) sm.pos[buf][tid] = pvalid ? rel_pos(preg, qbase) : kFar;
   };
 
-  f32x4 oacc[kDTiles][2];
+  f32x4 oacc[kDTiles][kSub];
 #pragma unroll
   for (int dt = 0; dt < kDTiles; ++dt)
 #pragma unroll
-    for (int s = 0; s < 2; ++s) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY};
-  f32x4 lacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};  // row sums (4 equal copies)
+    for (int s = 0; s < kSub; ++s) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[kSub];
+#pragma unroll
+  for (int s = 0; s < kSub; ++s) m_run[s] = -INFINITY;
+  f32x4 lacc[kSub];  // row sums (4 equal copies)
+#pragma unroll
+  for (int s = 0; s < kSub; ++s) lacc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
   const bf16x8 kOnes = {__bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f),
                         __bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f)};
 
@@ -346,17 +358,17 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
                         (a.window >= 0 && pos0 < last_rel - a.window);
 
     // S^T = K . Q^T
-    f32x4 sacc[4][2];
+    f32x4 sacc[4][kSub];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) sacc[kt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < kSub; ++s) sacc[kt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < kKSteps; ++ks) {
         const bf16x8 kop =
             __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&sm.k[buf][16 * kt + col][32 * ks + 8 * quad]));
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
+        for (int s = 0; s < kSub; ++s)
           sacc[kt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[s][ks], sacc[kt][s], 0, 0, 0);
       }
     }
@@ -367,16 +379,16 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
     // O and l; p = 2^(t - m_run) then stays below 2^kLazy.  Masked scores
     // become -inf in place (exp2 -> 0): no per-key branches, one shared
     // softmax, and tiles wholly inside every row's range skip the mask.
-    bf16x8 pop[2][2];
+    bf16x8 pop[kSub][2];
     {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
+      for (int s = 0; s < kSub; ++s) {
         f32x4 t[4];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) t[kt] = sacc[kt][s];
         if (masked) {
           // causal: key index <= the row's token; window: key pos >= row pos - W
-          const int32_t climit = ext ? t0 + row_tl[s] - base : kKeys;
+          const int32_t climit = ext ? t0 + (row_th[s] & 0xffff) - base : kKeys;
           const int32_t last = climit < count - 1 ? climit : count - 1;
           const int32_t thr = a.window >= 0 ? row_rel[s] - a.window : -kFar - 1;
 #pragma unroll
@@ -438,7 +450,7 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
             (lds_s16x4*)&sm.v[buf][32 * kk + 16 + 4 * quad + (col >> 2)][16 * dt + 4 * (col & 3)]);
         const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
+        for (int s = 0; s < kSub; ++s)
           oacc[dt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[s][kk], oacc[dt][s], 0, 0, 0);
       }
     // row sums of the same bf16 weights on the matrix cores (a ones operand):
@@ -446,7 +458,7 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+      for (int s = 0; s < kSub; ++s)
         lacc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kOnes, pop[s][kk], lacc[s], 0, 0, 0);
 
     if (it + 1 < n_tiles) commit(buf ^ 1);
@@ -455,19 +467,20 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 3 : 2) context_attention_k
 
   // normalise with the sink; store
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
+  for (int s = 0; s < kSub; ++s) {
     float l = lacc[s][0];
     float scale = 1.f;
     if (a.sinks) {
-      const float sink = a.sinks[row_head[s]] * kLog2e;
+      const float sink = a.sinks[row_th[s] >> 16] * kLog2e;
       const float m_f = fmaxf(m_run[s], sink);
       scale = m_run[s] == -INFINITY ? 0.f : exp2f(m_run[s] - m_f);
       l = l * scale + exp2f(sink - m_f);
     }
     const float inv = l > 0.f ? scale / l : 0.f;
-    if (!row_ok[s]) continue;
+    const int32_t row_token = row_th[s] & 0xffff, row_head = row_th[s] >> 16;
+    if (t0 + row_token >= qlen) continue;
     const int64_t at =
-        (qo0 + t0 + row_tl[s]) * a.o_st + static_cast<int64_t>(row_head[s]) * a.o_sh + 4 * quad;
+        (qo0 + t0 + row_token) * a.o_st + static_cast<int64_t>(row_head) * a.o_sh + 4 * quad;
 #pragma unroll
     for (int dt = 0; dt < kDTiles; ++dt) {
       const f32x4 o = oacc[dt][s] * inv;
@@ -528,9 +541,12 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
   if (n_segments == 0 || max_query_len == 0) return AKV_OK;
   if (head_dim != 64 && head_dim != 128)
     return fail(AKV_EINVAL, "akv_context_attention: head_dim %d (supported: 64, 128)", head_dim);
-  if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0 || kRows % (q_heads / kv_heads) != 0)
-    return fail(AKV_EINVAL, "akv_context_attention: %d q heads over %d KV heads (group must divide %d)",
-                q_heads, kv_heads, kRows);
+  // the group of q heads per KV head divides every block's row count; a
+  // row packs its q head into 15 bits
+  if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0 || 128 % (q_heads / kv_heads) != 0 ||
+      q_heads > 32767)
+    return fail(AKV_EINVAL, "akv_context_attention: %d q heads over %d KV heads (group must divide 128)",
+                q_heads, kv_heads);
   if (!valid_index_dtype(indptr_dtype) || !valid_index_dtype(indices_dtype) ||
       !valid_index_dtype(positions_dtype))
     return fail(AKV_EINVAL, "akv_context_attention: index vectors must be int32 or int64");
@@ -586,7 +602,7 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
   a.scale_log2 = scale * kLog2e;
   a.out_f32 = out_dtype == AKV_F32;
   a.group = q_heads / kv_heads;
-  a.tokens_per_block = kRows / a.group;
+  a.tokens_per_block = rows_per_block(head_dim) / a.group;
   const int64_t blocks = (max_query_len + a.tokens_per_block - 1) / a.tokens_per_block;
   if (blocks > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_context_attention: queries too long");
   const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(kv_heads), static_cast<unsigned>(n_segments));

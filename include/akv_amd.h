@@ -251,8 +251,9 @@ int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * sinks (opt.) f32 [q_heads] add e^sink to the softmax denominator.
  * q [Nq, q_heads, D], k_ext/v_ext [Nq, kv_heads, D], pool [slots, kv_heads, D]
  * bf16 with unit dim stride; out bf16 or f32 like q; D = 64 or 128;
- * q_heads / kv_heads divides 128.  indptrs / indices / positions: AKV_I32
- * or AKV_I64.  max_query_len: host bound on every segment's query count.
+ * q_heads / kv_heads divides 128, q_heads < 32768; scale > 0.  indptrs /
+ * indices / positions: AKV_I32 or AKV_I64.  max_query_len: host bound on
+ * every segment's query count.
  * Replaces the Triton extend attention launched by
  * ContextAttentionMetadata.forward with context positions,
  * akv/system/sglang/srt/layers/attention/context_backend.py:180-251 and
