@@ -91,7 +91,7 @@ _SIGNATURES = {
     ),
     "akv_gather_slots": (
         c_int32,
-        [c_int32, _P, c_int64, _P, _P, _P, c_int64, c_int64, _P, _P, _P],
+        [c_int32, _P, c_int64, c_int64, _P, _P, _P, c_int64, c_int64, _P, _P, _P],
     ),
     "akv_window_count": (
         c_int32,

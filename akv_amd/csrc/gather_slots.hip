@@ -8,7 +8,8 @@
 // request, segments of owner-row indices into that vector (occurrence
 // slots, copy sources, copy destinations, successor owners, retired pages,
 // SWA-released pages ...).  One launch resolves every segment of the batch:
-// element i of the concatenation gets slot(b, rows[i]), or -1 for row -1.
+// element i of the concatenation gets slot(b, rows[i]), or -1 for row -1
+// (and for a row or request id out of range: no read outside the pieces).
 // Elements [0, wide_count) go to `out_wide` (the slot dtype), the rest to
 // `out_narrow` (int32: the copy lists the Reposition reads).
 //
@@ -28,6 +29,7 @@ struct GatherArgs {
   const int64_t* segment_offsets;  // [S + 1]
   const int64_t* segment_requests;  // [S]
   const int64_t* rows;  // [total]
+  int64_t n_requests;
   int64_t n_segments;
   int64_t total;
   int64_t wide_count;
@@ -51,7 +53,7 @@ __global__ void __launch_bounds__(kThreads) gather_slots_kernel(const GatherArgs
   const int64_t b = a.segment_requests[lo];
   int64_t row = a.rows[i];
   int64_t v = -1;
-  if (row >= 0) {
+  if (row >= 0 && b >= 0 && b < a.n_requests) {
     const int64_t* src = a.sources + 6 * b;
 #pragma unroll
     for (int piece = 0; piece < 3; ++piece) {
@@ -72,21 +74,22 @@ __global__ void __launch_bounds__(kThreads) gather_slots_kernel(const GatherArgs
 }  // namespace
 }  // namespace akv
 
-extern "C" int akv_gather_slots(int32_t slot_dtype, const int64_t* sources, int64_t n_segments,
+extern "C" int akv_gather_slots(int32_t slot_dtype, const int64_t* sources, int64_t n_requests, int64_t n_segments,
                                 const int64_t* segment_offsets, const int64_t* segment_requests,
                                 const int64_t* rows, int64_t total, int64_t wide_count, void* out_wide,
                                 int32_t* out_narrow, void* stream) {
   using namespace akv;
   if (!valid_index_dtype(slot_dtype)) return fail(AKV_EINVAL, "akv_gather_slots: slot dtype must be int32 or int64");
-  if (total < 0 || n_segments < 0 || wide_count < 0 || wide_count > total)
+  if (total < 0 || n_requests < 0 || n_segments < 0 || wide_count < 0 || wide_count > total)
     return fail(AKV_EINVAL, "akv_gather_slots: invalid sizes");
   if (total == 0) return AKV_OK;
-  if (n_segments == 0 || !sources || !segment_offsets || !segment_requests || !rows ||
+  if (n_requests == 0 || n_segments == 0 || !sources || !segment_offsets || !segment_requests || !rows ||
       (wide_count && !out_wide) || (wide_count < total && !out_narrow))
     return fail(AKV_EINVAL, "akv_gather_slots: null pointer");
   const int64_t blocks = (total + kThreads - 1) / kThreads;
   if (blocks > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_gather_slots: too many elements");
-  GatherArgs a{sources, segment_offsets, segment_requests, rows, n_segments, total, wide_count, out_wide, out_narrow};
+  GatherArgs a{sources, segment_offsets, segment_requests, rows, n_requests, n_segments, total, wide_count, out_wide,
+               out_narrow};
   if (slot_dtype == AKV_I64)
     hipLaunchKernelGGL(gather_slots_kernel<int64_t>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
                        as_stream(stream), a);

@@ -181,6 +181,9 @@ extern "C" int akv_advance_ownership(
     if (canonical_rows[t] < -1 || canonical_rows[t] >= old_count || terminal_rows[t] < -1 ||
         terminal_rows[t] >= old_count)
       return fail(AKV_EINVAL, "akv_advance_ownership: state rows out of range");
+  for (int64_t t = 0; t < end; ++t)
+    if (terminal_occurrences[t] < 0 || terminal_occurrences[t] >= occurrence_count)
+      return fail(AKV_EINVAL, "akv_advance_ownership: terminal occurrence out of range");
 
   std::vector<int64_t> occ(occurrence_count);
   for (int64_t o = 0; o < occurrence_count; ++o) {

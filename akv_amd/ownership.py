@@ -101,7 +101,8 @@ class _Gather:
             lib = _lib.load()
             with _on_device(self.device):
                 rc = lib.akv_gather_slots(
-                    _SLOT_DTYPES[self.dtype], d_sources.data_ptr(), len(segments), d_offsets.data_ptr(),
+                    _SLOT_DTYPES[self.dtype], d_sources.data_ptr(), len(self.requests), len(segments),
+                    d_offsets.data_ptr(),
                     d_requests.data_ptr(), d_rows.data_ptr(), total, wide_total,
                     out_wide.data_ptr() if wide_total else None,
                     out_narrow.data_ptr() if total > wide_total else None, current_stream_handle(self.device))

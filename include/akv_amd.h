@@ -487,14 +487,16 @@ int akv_advance_ownership(
  * (AKV_I32 or AKV_I64 slots, all of slot_dtype); segment s covers elements
  * [segment_offsets[s], segment_offsets[s + 1]) and belongs to request
  * segment_requests[s].  Element i = slot of rows[i] in its request's
- * concatenated pieces, -1 for row -1; elements [0, wide_count) go to
+ * concatenated pieces (n_requests of them), -1 for row -1 or a row / request
+ * out of range; elements [0, wide_count) go to
  * out_wide (slot_dtype), the rest to out_narrow (int32).  One launch for a
  * whole batch; replaces the per-request torch.cat and indexing of
  * akv/system/sglang/srt/context_system/occurrence.py:733-767,795-798,856-864
  * and the batch concatenation of akv/system/sglang.patch:3174-3180.
  */
 int akv_gather_slots(int32_t slot_dtype, const int64_t* sources,
-                     int64_t n_segments, const int64_t* segment_offsets,
+                     int64_t n_requests, int64_t n_segments,
+                     const int64_t* segment_offsets,
                      const int64_t* segment_requests, const int64_t* rows,
                      int64_t total, int64_t wide_count, void* out_wide,
                      int32_t* out_narrow, void* stream);

@@ -72,8 +72,8 @@ def test_validation_rejects_before_any_device_work(lib):
     assert lib.akv_gather_slots(*zeros(lib.akv_gather_slots, a0=7)) == _lib.AKV_EINVAL
     assert "slot dtype" in _lib.last_error()
     assert lib.akv_gather_slots(*zeros(lib.akv_gather_slots)) == 0  # nothing to gather
-    assert lib.akv_gather_slots(*zeros(lib.akv_gather_slots, a6=5, a7=9)) == _lib.AKV_EINVAL
-    assert lib.akv_gather_slots(*zeros(lib.akv_gather_slots, a6=5, a7=5)) == _lib.AKV_EINVAL
+    assert lib.akv_gather_slots(*zeros(lib.akv_gather_slots, a7=5, a8=9)) == _lib.AKV_EINVAL
+    assert lib.akv_gather_slots(*zeros(lib.akv_gather_slots, a7=5, a8=5)) == _lib.AKV_EINVAL
     assert "null pointer" in _lib.last_error()
     assert lib.akv_plan_ownership(*zeros(lib.akv_plan_ownership, a0=4, a1=2, a2=1)) == _lib.AKV_EINVAL
     assert "Invalid occurrence ownership/query boundaries" in _lib.last_error()
