@@ -16,8 +16,10 @@ kernel's average launch in that timed region and its roofline against
 of the same workload.  ``other_configs`` measures the surrounding rows on
 their own workloads: the tiny and ragged-batch compactions, ascending slots,
 the decode step over the compacted metadata, the next turn's prefill
-attention, a multi-turn trajectory's occurrence binding, the compacted
-handoff copies and the page-16 copy-on-write batch.
+attention (GPT-OSS and Llama-3 layer shapes), a multi-turn trajectory's
+occurrence binding in one forward and in 4 chunked forwards with cache
+publication, the compacted handoff copies and the page-16 copy-on-write
+batch.
 """
 
 import argparse
@@ -579,11 +581,10 @@ def handoff_config(device, flush):
     return out
 
 
-def prefill_config(device, flush, extend=4096):
-    """Next turn's prefill over the compacted 32k GPT-OSS request: 4096 new
-    tokens attend to the 19441 kept tokens (positions with the dropped holes)
-    and causally to themselves; a full layer and a 128-window layer (64 q /
-    8 KV heads x 64, sinks)."""
+def _prefill(device, flush, *, hq, hkv, d, sinks, windows, extend=4096):
+    """Next turn's prefill over the compacted 32k request: ``extend`` new
+    tokens attend to its 19441 kept tokens (positions with the dropped
+    holes) and causally to themselves; one launch per layer kind."""
     from akv_amd import context_attention as ca
 
     w = synth.workload("gpt-oss-32k")
@@ -593,7 +594,6 @@ def prefill_config(device, flush, extend=4096):
     plen = len(kept_pos)
     nxt = int(lay.next_position)
     qpos = np.arange(nxt, nxt + extend, dtype=np.int64)
-    hq, hkv, d = 64, 8, 64
     slots = 2 * plen + 1
     g = torch.Generator(device=device)
     g.manual_seed(11)
@@ -602,7 +602,7 @@ def prefill_config(device, flush, extend=4096):
     ve = torch.randn((extend, hkv, d), generator=g, device=device).to(torch.bfloat16)
     kp = torch.randn((slots, hkv, d), generator=g, device=device).to(torch.bfloat16)
     vp = torch.randn((slots, hkv, d), generator=g, device=device).to(torch.bfloat16)
-    sinks = torch.randn(hq, generator=g, device=device)
+    sink_t = torch.randn(hq, generator=g, device=device) if sinks else None
     rng = np.random.default_rng(11)
     idx = torch.from_numpy(rng.permutation(np.arange(1, slots))[:plen].astype(np.int32)).to(device)
     qo = torch.tensor([0, extend], dtype=torch.int64, device=device)
@@ -613,21 +613,38 @@ def prefill_config(device, flush, extend=4096):
 
     def layer(window):
         return lambda: ca.extend_attention_fwd(q, ke, ve, out, kp, vp, qo, kv, idx, None, True, None, extend,
-                                               sm_scale=0.125, sliding_window_size=window, sinks=sinks,
+                                               sm_scale=d ** -0.5, sliding_window_size=window, sinks=sink_t,
                                                context_q_positions=qp, context_kv_positions=kpp)
 
     warm_full, cold_full = _time_steps(layer(-1), 10, 3, 10, flush)
-    warm_win, cold_win = _time_steps(layer(128), 20, 3, 10, flush)
     # causal flops: QK^T and PV, 2 flops per multiply-add each
     flops_full = 4 * hq * d * sum(plen + i + 1 for i in range(extend))
-    return {
-        "workload": f"gpt-oss-120b prefill of {extend} tokens over {plen} kept tokens (64 q / 8 KV heads x 64, sinks)",
+    r = {
         "full_layer_ms": round(warm_full, 4), "full_layer_p50_ms": round(percentile(cold_full, 50), 4),
         "full_layer_TFLOPs": round(flops_full / (warm_full / 1e3) / 1e12, 1),
         "full_layer_pct_mfma_bf16_peak": round(100 * flops_full / (warm_full / 1e3) / 2.5e15, 2),
-        "window128_layer_ms": round(warm_win, 4), "window128_layer_p50_ms": round(percentile(cold_win, 50), 4),
-        "kernel_launches_per_layer": 1,
     }
+    for window in windows:
+        warm_win, cold_win = _time_steps(layer(window), 20, 3, 10, flush)
+        r[f"window{window}_layer_ms"] = round(warm_win, 4)
+        r[f"window{window}_layer_p50_ms"] = round(percentile(cold_win, 50), 4)
+    r["kernel_launches_per_layer"] = 1
+    return r, plen
+
+
+def prefill_config(device, flush, extend=4096):
+    """GPT-OSS layers (64 q / 8 KV heads x 64, sinks): a full layer and a
+    128-window layer."""
+    r, plen = _prefill(device, flush, hq=64, hkv=8, d=64, sinks=True, windows=(128,), extend=extend)
+    return {"workload": f"gpt-oss-120b prefill of {extend} tokens over {plen} kept tokens "
+                        f"(64 q / 8 KV heads x 64, sinks)", **r}
+
+
+def prefill_llama_config(device, flush, extend=4096):
+    """Llama-3-8B layer shape (32 q / 8 KV heads x 128, no sinks, no window)
+    over the same request metadata."""
+    r, plen = _prefill(device, flush, hq=32, hkv=8, d=128, sinks=False, windows=(), extend=extend)
+    return {"workload": f"llama3-8b prefill of {extend} tokens over {plen} kept tokens (32 q / 8 KV heads x 128)", **r}
 
 
 def read_pmc_traffic():
@@ -885,7 +902,8 @@ def main():
         print("# secondary configurations ...", file=sys.stderr, flush=True)
         result["other_configs"] = [tiny_config(device, pipe.flush), ascending_slots_config(device, pipe.flush),
                                    ragged_config(device, pipe.flush), decode_consumer_config(device, pipe.flush),
-                                   prefill_config(device, pipe.flush), multistage_config(device, pipe.flush),
+                                   prefill_config(device, pipe.flush), prefill_llama_config(device, pipe.flush),
+                                   multistage_config(device, pipe.flush),
                                    chunked_config(device, pipe.flush), handoff_config(device, pipe.flush)]
         if not args.no_cow:
             print("# copy-on-write configuration ...", file=sys.stderr, flush=True)
