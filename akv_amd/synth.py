@@ -39,6 +39,12 @@ GPT_OSS_120B = Model(
     36, 8, 64, 64,
     dict(kind="yarn", base=150000.0, factor=32.0, original_max=4096, beta_fast=32.0, beta_slow=1.0),
 )
+# one rank's share of GPT-OSS-120B at tensor parallel 2 (4 of the 8 KV heads)
+GPT_OSS_120B_TP2 = Model(
+    "gpt-oss-120b TP=2 rank (36 layers, 4 KV heads, head_dim 64, YaRN)",
+    36, 4, 64, 64,
+    dict(kind="yarn", base=150000.0, factor=32.0, original_max=4096, beta_fast=32.0, beta_slow=1.0),
+)
 TINY = Model("tiny (2 layers, 2 KV heads, head_dim 64, plain RoPE)", 2, 2, 64, 64,
              dict(kind="plain", base=10000.0))
 LLAMA3_8B = Model(
@@ -248,6 +254,10 @@ def workload(name):
         # GPT-OSS-120B shape; 32768 tokens, 12 tool-result spans of 500-2000
         # tokens dropping ~40%
         return single_request_workload("gpt-oss-120b-32k", GPT_OSS_120B, 32768, 12, 500, 2000, 0.40,
+                                       seed=2)
+    if name == "gpt-oss-32k-tp2":
+        # the same request and events, one TP=2 rank's 4 KV heads
+        return single_request_workload("gpt-oss-120b-32k-tp2-rank", GPT_OSS_120B_TP2, 32768, 12, 500, 2000, 0.40,
                                        seed=2)
     if name == "llama3-cow-16":
         # Llama-3-8B shape, page 16: 16 requests share an 8192-token prefix

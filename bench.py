@@ -15,6 +15,7 @@ kernel's average launch in that timed region and its roofline against
 1 GiB read flush of L2 + the 256 MB MALL; the CPU oracle on a bounded sample
 of the same workload.  ``other_configs`` measures the surrounding rows on
 their own workloads: the tiny and ragged-batch compactions, ascending slots,
+one TP=2 rank's head share,
 the decode step over the compacted metadata, the next turn's prefill
 attention (GPT-OSS and Llama-3 layer shapes), a multi-turn trajectory's
 occurrence binding in one forward and in 4 chunked forwards with cache
@@ -201,6 +202,24 @@ def ascending_slots_config(device, flush):
         "reposition_pct_hbm_peak": round(100 * pipe.alg_bytes / (repo_warm / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
     }
     del pipe
+    return out
+
+
+def tp2_share_config(device, flush):
+    """One rank's share of the 32k GPT-OSS step at tensor parallel 2: the
+    same tokens and spans, 4 of the 8 KV heads (512 B K and V rows)."""
+    pipe = Pipeline("gpt-oss-32k-tp2", device)
+    warm, cold = _time_steps(pipe.step, 50, 10, 50, flush)
+    repo_warm, _ = _time_steps(pipe.reposition, 50, 10, 0, flush)
+    out = {
+        "workload": pipe.w.name, "moved": pipe.moved,
+        "step_ms_back_to_back": round(warm, 5), "step_p50_ms": round(percentile(cold, 50), 5),
+        "retained_kv_GBs": round(pipe.retained_bytes / (warm / 1e3) / 1e9, 1),
+        "reposition_ms": round(repo_warm, 5),
+        "reposition_pct_hbm_peak": round(100 * pipe.alg_bytes / (repo_warm / 1e3) / 1e9 / HBM_PEAK_GBS, 2),
+    }
+    del pipe
+    torch.cuda.empty_cache()
     return out
 
 
@@ -901,6 +920,7 @@ def main():
     if not args.reposition_only:
         print("# secondary configurations ...", file=sys.stderr, flush=True)
         result["other_configs"] = [tiny_config(device, pipe.flush), ascending_slots_config(device, pipe.flush),
+                                   tp2_share_config(device, pipe.flush),
                                    ragged_config(device, pipe.flush), decode_consumer_config(device, pipe.flush),
                                    prefill_config(device, pipe.flush), prefill_llama_config(device, pipe.flush),
                                    multistage_config(device, pipe.flush),
