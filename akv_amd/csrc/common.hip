@@ -1,4 +1,6 @@
 // Error state and version of the akv_amd C ABI.
+#include <string>
+
 #include "common.h"
 
 namespace akv {
@@ -9,12 +11,16 @@ std::string& last_error() {
 }
 
 int fail(int code, const char* fmt, ...) {
-  char buf[512];
-  va_list ap;
+  // sized to the message: some list every offending index
+  va_list ap, again;
   va_start(ap, fmt);
-  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_copy(again, ap);
+  const int len = vsnprintf(nullptr, 0, fmt, ap);
   va_end(ap);
-  last_error() = buf;
+  std::string msg(len > 0 ? static_cast<size_t>(len) : 0, '\0');
+  if (len > 0) vsnprintf(&msg[0], msg.size() + 1, fmt, again);
+  va_end(again);
+  last_error() = std::move(msg);
   return code;
 }
 

@@ -23,7 +23,7 @@ CACHE_BASE = 1_000_000  # cache-owned (borrowed) slots live above this
 
 
 def _program(rng, n):
-    k = int(rng.integers(1, 4))
+    k = int(rng.integers(1, 4 if n < 100 else 12))
     inserts = np.sort(rng.choice(np.arange(3, n), size=min(k, n - 3), replace=False))
     drops, offsets, drop_at = [], [0], []
     visible = np.full(n, INF, dtype=np.int64)
@@ -49,9 +49,9 @@ def _program(rng, n):
     return events, visible
 
 
-def make(seed):
+def make(seed, n_range=(10, 90), max_cuts=4):
     rng = np.random.default_rng(seed)
-    n = int(rng.integers(10, 90))
+    n = int(rng.integers(*n_range))
     while True:  # redraw programs whose Reposition finds no active token
         events, visible = _program(rng, n)
         try:
@@ -69,7 +69,8 @@ def make(seed):
     swa = rng.random(n) < 0.8 if rng.random() < 0.5 else None
     sc["match"] = dict(slots=cache[:n].astype(np.int64), positions=positions.astype(np.int32), resident=resident,
                        length=m, exact=int(rng.integers(0, m + 1)), swa=swa)
-    cuts = sorted(set(int(c) for c in rng.integers(m + 1, n, size=int(rng.integers(0, 4))))) if m + 1 < n else []
+    cuts = sorted(set(int(c) for c in rng.integers(m + 1, n, size=int(rng.integers(0, max_cuts))))) \
+        if m + 1 < n else []
     bounds = [m, *[c for c in cuts if m < c < n], n]
     # a recovery gap: the head of one forward's range is borrowed instead
     gap = None

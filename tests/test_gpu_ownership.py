@@ -116,3 +116,19 @@ def test_plan_bind_agrees_with_advance(device):
         assert torch.equal(bpairs.cpu(), adv.copy_position_pairs.cpu())
         checked += 1
     assert checked > 25
+
+
+def test_long_lifecycles_match_the_oracle(device):
+    """Prompts of 300-1500 tokens, up to 12 turns and 8 forwards, through the
+    HIP gather: the trace equals the oracle's."""
+    native = scenarios.NativeImpl(device)
+    oracle = scenarios.OracleImpl()
+    print("long ownership lifecycles", flush=True)
+    for seed in range(30):
+        sc = scenarios.make(5000 + seed, n_range=(300, 1500), max_cuts=8)
+        want = scenarios.run(sc, oracle)
+        got = scenarios.run(sc, native)
+        torch.cuda.synchronize()
+        assert [k for k, _ in got] == [k for k, _ in want], seed
+        for (name, a), (_, b) in zip(got, want):
+            assert _same(a, b), (seed, name)

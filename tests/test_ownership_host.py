@@ -117,3 +117,20 @@ def test_free_context_slots_splits_by_swa_residency(cpu_gather):
     ownership.free_context_slots(a, slots, None)
     ownership.free_context_slots(a, slots, torch.zeros(4, dtype=torch.bool))
     assert a.calls == [("free", [5, 7]), ("free_full", [6, 8]), ("free", [5, 6, 7, 8]), ("free_full", [5, 6, 7, 8])]
+
+
+def test_long_lifecycles_match_the_oracle(cpu_gather):
+    """Prompts of 300-1500 tokens, up to 12 Drop/Reposition turns and 8
+    forwards: the native planner's trace equals the oracle's."""
+    native = scenarios.NativeImpl(torch.device("cpu"))
+    oracle = scenarios.OracleImpl()
+    forwards = 0
+    for seed in range(30):
+        sc = scenarios.make(5000 + seed, n_range=(300, 1500), max_cuts=8)
+        want = scenarios.run(sc, oracle)
+        got = scenarios.run(sc, native)
+        assert [k for k, _ in got] == [k for k, _ in want], seed
+        for (name, a), (_, b) in zip(got, want):
+            assert _same(a, b), (seed, name)
+        forwards += sum(1 for k, _ in want if k.endswith(".keep"))
+    assert forwards > 60
