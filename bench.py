@@ -57,6 +57,8 @@ def parse_args():
                    help="time only the Reposition launch (for profiling runs)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy 1 GiB -> 1 GiB three times (scales rocprof byte counters)")
+    p.add_argument("--only", choices=["handoff", "prefill", "chunked"],
+                   help="run one secondary configuration alone and print its line (for profiling runs)")
     return p.parse_args()
 
 
@@ -793,6 +795,13 @@ def main():
     torch.cuda.set_device(device)
     if args.copy_calibration:
         copy_calibration(device)
+        return
+    if args.only:
+        scratch = torch.ones(1 << 28, dtype=torch.float32, device=device)
+        sink = torch.empty((), device=device)
+        flush = lambda: torch.sum(scratch, 0, out=sink)  # noqa: E731
+        run = {"handoff": handoff_config, "prefill": prefill_config, "chunked": chunked_config}[args.only]
+        print(json.dumps(run(device, flush)), flush=True)
         return
     pipe = Pipeline(args.workload, device)
     pipe.compaction()
