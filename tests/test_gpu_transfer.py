@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from akv_amd import synth, transfer
+from akv_amd import transfer
 
 pytestmark = pytest.mark.gpu
 
