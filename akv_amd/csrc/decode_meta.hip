@@ -16,7 +16,10 @@
 namespace akv {
 namespace {
 
-constexpr int kBlocksPerRequest = 8;
+// workgroups per request, and independent gathers each thread keeps in flight
+// (one row entry costs two dependent loads: raw id, then slot)
+constexpr int kBlocksPerRequest = 16;
+constexpr int kUnroll = 4;
 
 struct DecodeArgs {
   const int64_t* registry;
@@ -49,14 +52,26 @@ __global__ void __launch_bounds__(256) decode_indices_kernel(const DecodeArgs a)
   const int32_t* raw_row = row_pointer != 0 ? reinterpret_cast<const int32_t*>(row_pointer)
                                             : a.table + row * a.row_stride;
   const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < length; i += step) {
+  auto raw_of = [&](int64_t i) -> int64_t {
     const int64_t logical = start + i;
-    int64_t raw = logical;
-    if (pointer != 0) raw = logical < active ? raw_ids[logical] : prompt + logical - active;
-    int64_t slot = raw_row[raw];
+    if (pointer == 0) return logical;
+    return logical < active ? raw_ids[logical] : prompt + logical - active;
+  };
+  auto emit = [&](int64_t i, int64_t slot) {
     if (a.mapping) slot = load_index(a.mapping, a.mapping64, slot) * a.multiplier;
     store_index(a.output, a.output64, offset + i, slot);
+  };
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (; i + (kUnroll - 1) * step < length; i += kUnroll * step) {
+    int64_t raw[kUnroll], slot[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) raw[u] = raw_of(i + u * step);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) slot[u] = raw_row[raw[u]];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) emit(i + u * step, slot[u]);
   }
+  for (; i < length; i += step) emit(i, raw_row[raw_of(i)]);
 }
 
 struct WindowArgs {

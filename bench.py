@@ -312,6 +312,23 @@ def decode_consumer_config(device, flush):
         attention.decode_attention(q, pool.k[0], pool.v[0], win_indptr, win_idx, o, scale=0.125, max_len=129,
                                    sinks=sinks, workspace=ws)
 
+    # the step's own read metadata from the registry: kv_indptr + kv_indices
+    # for the full layer, window lengths + indptr + indices for the SWA layer
+    meta_indptr = torch.zeros(B + 1, dtype=torch.int32, device=device)
+    meta_idx = torch.full((inputs.kept_total + B,), -1, dtype=torch.int32, device=device)
+
+    def meta_full():
+        page_table.build_indptr(seq, meta_indptr)
+        registry.fill(rows, seq, meta_indptr, meta_idx)
+
+    def meta_window():
+        registry.fill_window(rows, seq, win_indptr, 128, win_idx)
+
+    meta_full()
+    if not (torch.equal(meta_indptr, out.kv_indptr.to(torch.int32)) and torch.equal(meta_idx, out.kv_indices)):
+        raise RuntimeError("decode metadata from the registry disagrees with the compaction's kv_indices")
+    warm_meta_full, cold_meta_full = _time_steps(meta_full, 50, 5, 20, flush)
+    warm_meta_win, cold_meta_win = _time_steps(meta_window, 50, 5, 20, flush)
     warm_full, cold_full = _time_steps(full, 20, 5, 20, flush)
     warm_win, cold_win = _time_steps(windowed, 50, 5, 20, flush)
     keys = inputs.kept_total + B
@@ -323,6 +340,14 @@ def decode_consumer_config(device, flush):
         "full_layer_kv_GBs": round(kv_bytes / (warm_full / 1e3) / 1e9, 1),
         "window128_layer_ms": round(warm_win, 5), "window128_layer_p50_ms": round(percentile(cold_win, 50), 5),
         "kernel_launches_per_layer": 2,
+        "metadata": {
+            "full_ms": round(warm_meta_full, 5), "full_p50_ms": round(percentile(cold_meta_full, 50), 5),
+            "full_p99_ms": round(percentile(cold_meta_full, 99), 5),
+            "window128_ms": round(warm_meta_win, 5),
+            "window128_p50_ms": round(percentile(cold_meta_win, 50), 5),
+            "window128_p99_ms": round(percentile(cold_meta_win, 99), 5),
+            "kernel_launches": {"full": 2, "window128": 3},
+        },
     }
 
 
