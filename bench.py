@@ -57,7 +57,7 @@ def parse_args():
                    help="time only the Reposition launch (for profiling runs)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy 1 GiB -> 1 GiB three times (scales rocprof byte counters)")
-    p.add_argument("--only", choices=["handoff", "prefill", "chunked", "decode"],
+    p.add_argument("--only", choices=["handoff", "prefill", "prefill-llama", "chunked", "decode"],
                    help="run one secondary configuration alone and print its line (for profiling runs)")
     return p.parse_args()
 
@@ -825,8 +825,8 @@ def main():
         scratch = torch.ones(1 << 28, dtype=torch.float32, device=device)
         sink = torch.empty((), device=device)
         flush = lambda: torch.sum(scratch, 0, out=sink)  # noqa: E731
-        run = {"handoff": handoff_config, "prefill": prefill_config, "chunked": chunked_config,
-               "decode": decode_consumer_config}[args.only]
+        run = {"handoff": handoff_config, "prefill": prefill_config, "prefill-llama": prefill_llama_config,
+               "chunked": chunked_config, "decode": decode_consumer_config}[args.only]
         print(json.dumps(run(device, flush)), flush=True)
         return
     pipe = Pipeline(args.workload, device)
