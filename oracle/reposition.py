@@ -29,6 +29,10 @@ elements (independent of the vectorised gather/scatter code), the identity
 (-x2, x1), bitwise V/tail copies, and ``skip_unmapped`` leaving the
 destination untouched.  A dropped term, a swapped sign or a swapped cos/sin
 half fails the closed-form rotation checks.
+
+Parity unpinned: NaN payloads.  A same-position copy here keeps the source
+bits; the reference's fp32 round trip may canonicalise a NaN's payload.  The
+checks use finite inputs only.
 """
 
 import numpy as np
