@@ -102,6 +102,11 @@ _SIGNATURES = {
         [c_int64, _P, _P, _P, c_int64, _P, _P, _P, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
          _P, _P],
     ),
+    "akv_window_compile_bounded": (
+        c_int32,
+        [c_int64, _P, _P, _P, c_int64, _P, _P, _P, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P,
+         _P, _P],
+    ),
     "akv_plan_count": (
         c_int32,
         [c_int64, _P, c_int64, _P, _P, c_int64, _P, _P, c_int64, _P, _P],

@@ -47,9 +47,11 @@ void require(bool ok, const char* message) {
 
 void fail_runtime(const char* message) { throw std::runtime_error(message); }
 
-// Output sink: counts, or fills caller arrays of the counted sizes.
+// Output sink: counts, or fills caller arrays of the counted sizes, or
+// (bounded) fills what fits in the caller's capacities and counts the rest.
 struct Sink {
   bool fill = false;
+  bool bounded = false;
   int64_t occurrences = 0, segments = 0, keys = 0, first_final = 0;
   int32_t* occ_raw = nullptr;
   int32_t* occ_pos = nullptr;
@@ -66,25 +68,33 @@ struct Sink {
   }
   void occurrence(int32_t raw, int32_t pos) {
     if (fill) {
-      if (occurrences >= cap_occurrences) overflow();
-      occ_raw[occurrences] = raw;
-      occ_pos[occurrences] = pos;
+      if (occurrences < cap_occurrences) {
+        occ_raw[occurrences] = raw;
+        occ_pos[occurrences] = pos;
+      } else if (!bounded) {
+        overflow();
+      }
     }
     ++occurrences;
   }
   void key(int32_t id) {
     if (fill) {
-      if (keys >= cap_keys) overflow();
-      key_occ[keys] = id;
+      if (keys < cap_keys)
+        key_occ[keys] = id;
+      else if (!bounded)
+        overflow();
     }
     ++keys;
   }
   void segment(int32_t start, int32_t end) {
     if (fill) {
-      if (segments >= cap_segments) overflow();
-      seg_start[segments] = start;
-      seg_end[segments] = end;
-      key_offsets[segments + 1] = static_cast<int32_t>(keys);
+      if (segments < cap_segments) {
+        seg_start[segments] = start;
+        seg_end[segments] = end;
+        key_offsets[segments + 1] = static_cast<int32_t>(keys);
+      } else if (!bounded) {
+        overflow();
+      }
     }
     ++segments;
   }
@@ -202,6 +212,24 @@ bool null_inputs(const int32_t* birth, const int32_t* stages, const int32_t* off
   return !birth || !stages || !offsets || !expiry || !terminal;
 }
 
+Sink fill_sink(const int64_t* capacities, int32_t* occ_raw, int32_t* occ_pos, int32_t* terminal_occ,
+               int32_t* seg_start, int32_t* seg_end, int32_t* key_offsets, int32_t* key_occ) {
+  Sink sink;
+  sink.fill = true;
+  sink.cap_occurrences = capacities[0];
+  sink.cap_segments = capacities[1];
+  sink.cap_keys = capacities[2];
+  sink.occ_raw = occ_raw;
+  sink.occ_pos = occ_pos;
+  sink.terminal_occ = terminal_occ;
+  sink.seg_start = seg_start;
+  sink.seg_end = seg_end;
+  sink.key_offsets = key_offsets;
+  sink.key_occ = key_occ;
+  key_offsets[0] = 0;
+  return sink;
+}
+
 }  // namespace
 }  // namespace akv
 
@@ -246,23 +274,49 @@ extern "C" int akv_window_compile(int64_t n, const int32_t* birth_positions, con
             query_start, query_end};
   // one replay: every write is bounded by the caller's counts, and the
   // counts must come out exact
-  Sink sink;
-  sink.fill = true;
-  sink.cap_occurrences = counts[0];
-  sink.cap_segments = counts[1];
-  sink.cap_keys = counts[2];
-  sink.occ_raw = occurrence_raw_tokens;
-  sink.occ_pos = occurrence_positions;
-  sink.terminal_occ = terminal_occurrences;
-  sink.seg_start = segment_query_starts;
-  sink.seg_end = segment_query_ends;
-  sink.key_offsets = segment_key_offsets;
-  sink.key_occ = segment_key_occurrences;
-  if (counts[1] < 0) return fail(AKV_EINVAL, "akv_window_compile: output capacities do not match the window");
-  segment_key_offsets[0] = 0;
+  if (counts[0] < 0 || counts[1] < 0 || counts[2] < 0)
+    return fail(AKV_EINVAL, "akv_window_compile: output capacities do not match the window");
+  Sink sink = fill_sink(counts, occurrence_raw_tokens, occurrence_positions, terminal_occurrences,
+                        segment_query_starts, segment_query_ends, segment_key_offsets, segment_key_occurrences);
   const int rc = run(in, sink);
   if (rc) return rc;
   if (sink.occurrences != counts[0] || sink.segments != counts[1] || sink.keys != counts[2])
     return fail(AKV_EINVAL, "akv_window_compile: output capacities do not match the window");
+  return AKV_OK;
+}
+
+extern "C" int akv_window_compile_bounded(int64_t n, const int32_t* birth_positions, const int32_t* birth_stages,
+                                          const int32_t* transition_offsets, int64_t stage_count,
+                                          const int32_t* transition_raw_tokens,
+                                          const int32_t* transition_old_positions,
+                                          const int32_t* transition_new_positions, const int32_t* visible_until,
+                                          const int32_t* terminal_positions, int64_t query_start,
+                                          int64_t query_end, const int64_t* capacities, int64_t* counts,
+                                          int32_t* occurrence_raw_tokens, int32_t* occurrence_positions,
+                                          int32_t* terminal_occurrences, int32_t* segment_query_starts,
+                                          int32_t* segment_query_ends, int32_t* segment_key_offsets,
+                                          int32_t* segment_key_occurrences) {
+  using namespace akv;
+  if (!capacities || !counts ||
+      null_inputs(birth_positions, birth_stages, transition_offsets, visible_until, terminal_positions) ||
+      !occurrence_raw_tokens || !occurrence_positions || !terminal_occurrences || !segment_query_starts ||
+      !segment_query_ends || !segment_key_offsets || !segment_key_occurrences)
+    return fail(AKV_EINVAL, "akv_window_compile_bounded: null host pointer");
+  if (capacities[0] < 0 || capacities[1] < 0 || capacities[2] < 0)
+    return fail(AKV_EINVAL, "akv_window_compile_bounded: negative capacity");
+  Inputs in{n, birth_positions, birth_stages, transition_offsets, stage_count, transition_raw_tokens,
+            transition_old_positions, transition_new_positions, visible_until, terminal_positions,
+            query_start, query_end};
+  // one replay: writes what fits, counts everything (a count above its
+  // capacity means the arrays are incomplete)
+  Sink sink = fill_sink(capacities, occurrence_raw_tokens, occurrence_positions, terminal_occurrences,
+                        segment_query_starts, segment_query_ends, segment_key_offsets, segment_key_occurrences);
+  sink.bounded = true;
+  const int rc = run(in, sink);
+  if (rc) return rc;
+  counts[0] = sink.occurrences;
+  counts[1] = sink.segments;
+  counts[2] = sink.keys;
+  counts[3] = sink.first_final;
   return AKV_OK;
 }

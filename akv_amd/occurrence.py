@@ -53,8 +53,13 @@ def _i32p(t):
     return ctypes.c_void_p(t.data_ptr()) if t.numel() else None
 
 
-def compile_occurrence_window(layout, full_token_visible_until, terminal_positions, *, query_start, query_end):
-    """Same ordered plan as the reference, from request-local CPU int32 arrays."""
+def compile_occurrence_window(layout, full_token_visible_until, terminal_positions, *, query_start, query_end,
+                             keys_capacity=None):
+    """Same ordered plan as the reference, from request-local CPU int32 arrays.
+
+    ``keys_capacity`` (optional) sizes the first replay's key array; the
+    default is four keys per token before ``query_end``.
+    """
     tensors = (
         layout.birth_positions,
         layout.birth_stages,
@@ -84,24 +89,40 @@ def compile_occurrence_window(layout, full_token_visible_until, terminal_positio
     lib = _lib.load()
     args = (n, _i32p(birth), _i32p(stages), _i32p(offsets), len(offsets) - 1, _i32p(changed), _i32p(old),
             _i32p(new), _i32p(expiry), _i32p(terminal), int(query_start), int(query_end))
+    # one replay into arrays sized by the bounds (occurrences <= n + transitions,
+    # segments <= queries) and a guess for the keys; a second, exact replay
+    # only when the keys outgrow the guess
+    caps = np.array([n + len(changed), int(query_end) - int(query_start),
+                     keys_capacity if keys_capacity is not None else 4 * int(query_end)], dtype=np.int64)
     counts = np.zeros(4, dtype=np.int64)
-    _lib.check(lib.akv_window_count(*args, counts.ctypes.data), "akv_window_count")
+    out = _window_arrays(n, caps)
+    rc = lib.akv_window_compile_bounded(*args, caps.ctypes.data, counts.ctypes.data, *_window_ptrs(out))
+    _lib.check(rc, "akv_window_compile_bounded")
+    if (counts[:3] > caps).any():
+        out = _window_arrays(n, counts)
+        rc = lib.akv_window_compile(*args, counts.ctypes.data, *_window_ptrs(out))
+        _lib.check(rc, "akv_window_compile")
     occ, segs, keys, first_final = (int(x) for x in counts)
-    i32 = torch.int32
-    out = dict(
-        occurrence_raw_tokens=torch.empty(occ, dtype=i32),
-        occurrence_positions=torch.empty(occ, dtype=i32),
-        terminal_occurrences=torch.empty(n, dtype=i32),
-        segment_query_starts=torch.empty(segs, dtype=i32),
-        segment_query_ends=torch.empty(segs, dtype=i32),
-        segment_key_offsets=torch.empty(segs + 1, dtype=i32),
-        segment_key_occurrences=torch.empty(keys, dtype=i32),
-    )
-    rc = lib.akv_window_compile(*args, counts.ctypes.data, *(out[k].data_ptr() for k in (
-        "occurrence_raw_tokens", "occurrence_positions", "terminal_occurrences", "segment_query_starts",
-        "segment_query_ends", "segment_key_offsets", "segment_key_occurrences")))
-    _lib.check(rc, "akv_window_compile")
-    return OccurrenceWindow(birth_occurrences=torch.arange(n, dtype=i32), first_final_occurrence=first_final, **out)
+    out = {k: v[: {"occurrence_raw_tokens": occ, "occurrence_positions": occ, "terminal_occurrences": n,
+                   "segment_query_starts": segs, "segment_query_ends": segs, "segment_key_offsets": segs + 1,
+                   "segment_key_occurrences": keys}[k]] for k, v in out.items()}
+    return OccurrenceWindow(birth_occurrences=torch.arange(n, dtype=torch.int32), first_final_occurrence=first_final,
+                            **out)
+
+
+_WINDOW_FIELDS = ("occurrence_raw_tokens", "occurrence_positions", "terminal_occurrences", "segment_query_starts",
+                  "segment_query_ends", "segment_key_offsets", "segment_key_occurrences")
+
+
+def _window_arrays(n, sizes):
+    occ, segs, keys = (int(x) for x in sizes[:3])
+    lengths = (occ, occ, n, segs, segs, segs + 1, keys)
+    return {k: torch.empty(m, dtype=torch.int32) for k, m in zip(_WINDOW_FIELDS, lengths)}
+
+
+def _window_ptrs(out):
+    # never empty: a window has at least one occurrence, segment and key
+    return tuple(ctypes.c_void_p(out[k].data_ptr()) for k in _WINDOW_FIELDS)
 
 
 # ---------------------------------------------------------------------------

@@ -322,6 +322,37 @@ int akv_window_compile(int64_t n, const int32_t* birth_positions,
                        int32_t* segment_key_occurrences);
 
 /*
+ * The same window in one replay: fills the output arrays up to
+ * capacities[3] = {occurrences, segments, keys} (terminal_occurrences [n],
+ * segment_key_offsets [segments capacity + 1]) and writes the exact
+ * counts[4] as akv_window_count does.  When a count exceeds its capacity
+ * the arrays are incomplete and the caller compiles again with those
+ * counts.  Occurrences never exceed n + offsets[stage_count] (a token gets
+ * a new version only after a transition moved it) and segments never
+ * exceed query_end - query_start.  Replaces the count + fill pair for
+ * compile_occurrence_window,
+ * akv/system/sglang/srt/context_system/occurrence.py:112-265.
+ */
+int akv_window_compile_bounded(int64_t n, const int32_t* birth_positions,
+                               const int32_t* birth_stages,
+                               const int32_t* transition_offsets,
+                               int64_t stage_count,
+                               const int32_t* transition_raw_tokens,
+                               const int32_t* transition_old_positions,
+                               const int32_t* transition_new_positions,
+                               const int32_t* visible_until,
+                               const int32_t* terminal_positions,
+                               int64_t query_start, int64_t query_end,
+                               const int64_t* capacities, int64_t* counts,
+                               int32_t* occurrence_raw_tokens,
+                               int32_t* occurrence_positions,
+                               int32_t* terminal_occurrences,
+                               int32_t* segment_query_starts,
+                               int32_t* segment_query_ends,
+                               int32_t* segment_key_offsets,
+                               int32_t* segment_key_occurrences);
+
+/*
  * Device bytes of the scratch buffer akv_bind_occurrences needs.
  */
 int64_t akv_bind_workspace_bytes(int32_t n_requests, int64_t max_occurrences);

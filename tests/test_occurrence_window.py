@@ -121,3 +121,28 @@ def test_reference_messages():
         ow.compile_occurrence_window(lay, vis, lay.birth_positions, query_start=0, query_end=6)
     with pytest.raises(ValueError, match="one-dimensional CPU int32"):
         ow.compile_occurrence_window(lay, vis.long(), lay.positions, query_start=0, query_end=6)
+
+
+@pytest.mark.parametrize("keys_capacity", [None, 1])
+def test_single_replay_and_its_fallback_match_the_oracle_on_query_windows(keys_capacity):
+    """The one-replay compile (bounded arrays) and, when its key guess is too
+    small, the exact second replay give the oracle's window for arbitrary
+    query ranges (chunked forwards)."""
+    rng = np.random.default_rng(11)
+    for _ in range(60):
+        n = int(rng.integers(8, 120))
+        events, visible = _program(rng, n)
+        ref = ev.compile_context_layout(*(np.asarray(events[k]) for k in events))
+        qs = int(rng.integers(0, n - 1))
+        qe = int(rng.integers(qs + 1, n + 1))
+        want = occ.compile_window(ref, visible, query_start=qs, query_end=qe)
+        lay = _torch_layout(events)
+        vis = torch.from_numpy(np.minimum(visible, 2**31 - 1).astype(np.int32))
+        got = ow.compile_occurrence_window(lay, vis, lay.positions, query_start=qs, query_end=qe,
+                                           keys_capacity=keys_capacity)
+        for field, key in (("occurrence_raw_tokens", "raw"), ("occurrence_positions", "pos"),
+                           ("terminal_occurrences", "terminal"), ("segment_key_occurrences", "keys"),
+                           ("segment_query_starts", "starts"), ("segment_query_ends", "ends"),
+                           ("segment_key_offsets", "key_offsets")):
+            np.testing.assert_array_equal(getattr(got, field).numpy(), want[key], err_msg=field)
+        assert got.first_final_occurrence <= got.occurrence_count
