@@ -20,9 +20,11 @@
 // G q heads of the group packed as rows: row r = token * G + head; R = 256
 // rows at head_dim 64 (4 waves x 64 rows, so each wave's reads of a K/V tile
 // from LDS feed 64 rows), 128 at head_dim 128 (4 waves x 32 rows).  Per
-// 64-key tile (K and V key-major in LDS, double buffered, the next tile's
-// global loads -- and the slots of the tile after it -- in flight during
-// this tile's math), for a wave's W rows:
+// 64-key tile (K and V key-major in LDS with XOR-swizzled 16 B chunks,
+// double buffered; the next tile's rows stream straight from HBM into LDS
+// with global_load_lds_dwordx4 -- no staging registers -- and the slots of
+// the tile after it are fetched, all during this tile's math), for a wave's
+// W rows:
 //   S^T[64 keys x W rows] = K . Q^T           v_mfma_f32_16x16x32_bf16
 //   online softmax per row (column of S^T) in the exp2 domain, the running
 //   maximum moving only when a tile exceeds it by 2^8 (lazy rescale)
@@ -129,10 +131,23 @@ __device__ __forceinline__ u32x4 load16b(const char* p) {
 
 template <int D>
 struct Smem {
-  __bf16 k[2][kKeys][D + 8];   // key-major K tile, rows padded by 16 B
-  __bf16 v[2][kKeys][D + 8];   // key-major V tile, read transposed (ds_read_b64_tr_b16)
-  int32_t pos[2][kKeys];       // key positions relative to the block's first query
+  __bf16 k[2][kKeys][D];   // key-major K tile, 16 B chunks swizzled per row (swz_k)
+  __bf16 v[2][kKeys][D];   // key-major V tile, read transposed (ds_read_b64_tr_b16), swizzled (swz_v)
+  int32_t pos[2][kKeys];   // key positions relative to the block's first query
 };
+
+// Chunk swizzles: logical 16 B chunk c of row r lives at chunk c ^ swz(r).
+// K (16 B operand reads, 16 rows per lane group): distinct banks for the 16
+// rows of a read.  V (8 B transposed reads, 4 rows x 32 B per 16 lanes, 8
+// rows per 32 lanes): bit 0 clear so a row's chunk pair stays adjacent, and
+// distinct bank groups for 8 consecutive rows.  At head_dim 64 a row is half
+// the 64 banks (rows of opposite parity use opposite halves).
+template <int D>
+__device__ __forceinline__ int swz_k(int r) { return D == 64 ? (r >> 1) & 7 : r & 15; }
+template <int D>
+__device__ __forceinline__ int swz_v(int r) { return D == 64 ? r & 6 : (r & 7) << 1; }
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int32_t kFar = 1 << 30;  // relative positions are clamped to [-kFar, kFar]
 
@@ -145,7 +160,6 @@ template <int D, typename IdxT, typename PosT, bool POS>
 __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const CtxArgs a) {
   constexpr int kSub = sub_tiles(D);
   constexpr int kChunks = D / 8;               // 16 B chunks per key row
-  constexpr int kRounds = kChunks / 8;         // (key pair, chunk) items per thread
   constexpr int kKSteps = D / 32;              // MFMA k-steps over head dims
   constexpr int kDTiles = D / 16;              // O^T row tiles
   __shared__ __attribute__((aligned(16))) Smem<D> sm;
@@ -240,64 +254,54 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
     }
   }
 
-  // tile staging: thread item u = key pair p (keys 2p, 2p+1) x 16 B chunk cc,
-  // for K and V.  Prefix slots are fetched one tile ahead of their rows.
+  // tile staging straight into LDS (global_load_lds_dwordx4: lane l of a
+  // wave instruction fills bytes 16 l of a 1 KiB block).  Block b of a tile
+  // holds rows kRowsPerBlock b ..; lane l writes row kRowsPerBlock b + l /
+  // kChunks at chunk position l % kChunks, i.e. logical chunk (l % kChunks)
+  // ^ swz(row) of that key, which it loads.  Each wave fills kBlocksPerWave
+  // blocks of K and of V.  Prefix slots are fetched one tile ahead.
+  constexpr int kRowsPerBlock = 1024 / (2 * D);
+  constexpr int kBlocksPerWave = kKeys / kRowsPerBlock / 4;
   using SlotT = typename std::conditional<sizeof(IdxT) == 4, uint32_t, int64_t>::type;
-  SlotT slot[kRounds][2];
-  u32x4 kreg[kRounds][2], vreg[kRounds][2];
+  SlotT slot[kBlocksPerWave];
   int64_t preg = 0;  // raw position of key tid of the staged tile
   bool pvalid = false;
+  const int my_row = lane / kChunks;   // row within a block
+  const int my_pos = lane % kChunks;   // chunk position within the row
   auto fetch_slots = [&](int it) {
     // keys past the prefix read the last prefix row (finite data, masked out)
     const int32_t base = tile_base(it);
 #pragma unroll
-    for (int u = 0; u < kRounds; ++u) {
-      const int p = (tid + kThreads * u) / kChunks;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int32_t j = base + 2 * p + e;
-        slot[u][e] = static_cast<SlotT>(slots[j < plen ? j : plen - 1]);
-      }
+    for (int u = 0; u < kBlocksPerWave; ++u) {
+      const int32_t j = base + (kBlocksPerWave * wave + u) * kRowsPerBlock + my_row;
+      slot[u] = static_cast<SlotT>(slots[j < plen ? j : plen - 1]);
     }
   };
-  auto stage = [&](int it) {
+  auto stage = [&](int it, int buf) {
     // branch-free: keys past the end read the last valid row (masked out later)
     const bool ext = it >= n_pref;
     const int32_t base = tile_base(it);
-    // addresses: one 32 x 32 -> 64-bit multiply-add each (row index and byte
-    // stride fit 32 bits: the host bounds strides to 31 bits of elements)
-    if (ext) {
 #pragma unroll
-      for (int u = 0; u < kRounds; ++u) {
-        const int c = tid + kThreads * u;
-        const int p = c / kChunks;
-        const int cc = c - p * kChunks;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int32_t j = base + 2 * p + e;
-          const uint64_t off = static_cast<uint32_t>(j < e_hi ? j : e_hi - 1);
-          kreg[u][e] = load16b(kext_b + 16 * cc + off * ke_sb);
-          vreg[u][e] = load16b(vext_b + 16 * cc + off * ve_sb);
-        }
+    for (int u = 0; u < kBlocksPerWave; ++u) {
+      const int blk = kBlocksPerWave * wave + u;
+      const int r = blk * kRowsPerBlock + my_row;
+      const int ck = my_pos ^ swz_k<D>(r), cv = my_pos ^ swz_v<D>(r);
+      const char *krow, *vrow;
+      if (ext) {
+        const int32_t j = base + r;
+        const uint64_t off = static_cast<uint32_t>(j < e_hi ? j : e_hi - 1);
+        krow = kext_b + off * ke_sb;
+        vrow = vext_b + off * ve_sb;
+      } else if constexpr (sizeof(IdxT) == 4) {
+        const uint64_t so = static_cast<uint32_t>(slot[u]);
+        krow = kpool_b + so * kp_sb;
+        vrow = vpool_b + so * vp_sb;
+      } else {
+        krow = reinterpret_cast<const char*>(kpool + slot[u] * a.kp_ss);
+        vrow = reinterpret_cast<const char*>(vpool + slot[u] * a.vp_ss);
       }
-    } else {
-#pragma unroll
-      for (int u = 0; u < kRounds; ++u) {
-        const int c = tid + kThreads * u;
-        const int p = c / kChunks;
-        const int cc = c - p * kChunks;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          if constexpr (sizeof(IdxT) == 4) {
-            const uint64_t so = static_cast<uint32_t>(slot[u][e]);
-            kreg[u][e] = load16b(kpool_b + 16 * cc + so * kp_sb);
-            vreg[u][e] = load16b(vpool_b + 16 * cc + so * vp_sb);
-          } else {
-            kreg[u][e] = load16(kpool + slot[u][e] * a.kp_ss + 8 * cc);
-            vreg[u][e] = load16(vpool + slot[u][e] * a.vp_ss + 8 * cc);
-          }
-        }
-      }
+      __builtin_amdgcn_global_load_lds(krow + 16 * ck, (lds_void*)(&sm.k[buf][blk * kRowsPerBlock][0]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vrow + 16 * cv, (lds_void*)(&sm.v[buf][blk * kRowsPerBlock][0]), 16, 0, 0);
     }
     if (tid < kKeys) {
       // loaded now, converted at commit: no wait on the tile's row loads here
@@ -308,18 +312,11 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
       preg = ext ? qpos_of(jc) : kpos_of(jc);
     }
   };
+  // positions of the staged tile, then wait for its direct loads (vmcnt) so
+  // the barrier that follows publishes the whole tile
   auto commit = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < kRounds; ++u) {
-      const int c = tid + kThreads * u;
-      const int p = c / kChunks;
-      const int cc = c - p * kChunks;
-      *reinterpret_cast<u32x4*>(&sm.k[buf][2 * p][8 * cc]) = kreg[u][0];
-      *reinterpret_cast<u32x4*>(&sm.k[buf][2 * p + 1][8 * cc]) = kreg[u][1];
-      *reinterpret_cast<u32x4*>(&sm.v[buf][2 * p][8 * cc]) = vreg[u][0];
-      *reinterpret_cast<u32x4*>(&sm.v[buf][2 * p + 1][8 * cc]) = vreg[u][1];
-    }
     if (tid < kKeys) sm.pos[buf][tid] = pvalid ? rel_pos(preg, qbase) : kFar;
+    __builtin_amdgcn_s_waitcnt(0);
   };
 
   f32x4 oacc[kDTiles][kSub];
@@ -337,14 +334,14 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
                         __bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f)};
 
   if (n_pref > 0) fetch_slots(0);
-  stage(0);
+  stage(0, 0);
   if (1 < n_pref) fetch_slots(1);
   commit(0);
   __syncthreads();
   for (int it = 0; it < n_tiles; ++it) {
     const int buf = it & 1;
     if (it + 1 < n_tiles) {
-      stage(it + 1);
+      stage(it + 1, buf ^ 1);
       if (it + 2 < n_pref) fetch_slots(it + 2);
     }
     const bool ext = it >= n_pref;
@@ -365,8 +362,9 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
       for (int s = 0; s < kSub; ++s) sacc[kt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < kKSteps; ++ks) {
-        const bf16x8 kop =
-            __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&sm.k[buf][16 * kt + col][32 * ks + 8 * quad]));
+        const int krow = 16 * kt + col;
+        const bf16x8 kop = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const u32x4*>(&sm.k[buf][krow][8 * ((4 * ks + quad) ^ swz_k<D>(krow))]));
 #pragma unroll
         for (int s = 0; s < kSub; ++s)
           sacc[kt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[s][ks], sacc[kt][s], 0, 0, 0);
@@ -444,10 +442,13 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
         // transposing read: lane col of group quad receives V[key][16dt + col]
         // for keys 32kk + 4 quad + i (i < 4), then 32kk + 16 + 4 quad + i;
         // source lane col supplies row key0 + col / 4, dims 16dt + 4 (col % 4) ..+3
+        // (logical element 16dt + 4(col%4) = chunk 2dt + (col%4)/2, half col%2)
+        const int vr0 = 32 * kk + 4 * quad + (col >> 2), vr1 = vr0 + 16;
+        const int vc = 2 * dt + ((col & 3) >> 1), vh = 4 * (col & 1);
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)&sm.v[buf][32 * kk + 4 * quad + (col >> 2)][16 * dt + 4 * (col & 3)]);
+            (lds_s16x4*)&sm.v[buf][vr0][8 * (vc ^ swz_v<D>(vr0)) + vh]);
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)&sm.v[buf][32 * kk + 16 + 4 * quad + (col >> 2)][16 * dt + 4 * (col & 3)]);
+            (lds_s16x4*)&sm.v[buf][vr1][8 * (vc ^ swz_v<D>(vr1)) + vh]);
         const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int s = 0; s < kSub; ++s)
