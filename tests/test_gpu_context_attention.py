@@ -84,11 +84,12 @@ def test_segments_match_oracle(device, d, hq, hkv, window, positions, with_sinks
             assert err <= TOL, f"segment {s} (q {Q_LENS[s]}, prefix {P_LENS[s]}) max err {err}"
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("idx_dtype,pos_dtype,indptr_dtype", [(torch.int64, torch.int32, torch.int32),
                                                               (torch.int32, torch.int32, torch.int64)])
-def test_index_dtypes(device, idx_dtype, pos_dtype, indptr_dtype):
+def test_index_dtypes(device, idx_dtype, pos_dtype, indptr_dtype, d):
     """int32 / int64 indices, positions and indptrs take their own kernel paths."""
-    d, hq, hkv = 64, 16, 2
+    hq, hkv = 16, 2
     c = _case(device, hq, hkv, d, [33, 70], [100, 9], seed=31)
     dv = c["dev"]
     qo = torch.from_numpy(c["qo"]).to(indptr_dtype).to(device)
@@ -103,6 +104,34 @@ def test_index_dtypes(device, idx_dtype, pos_dtype, indptr_dtype):
     want = oat.context_attention(_f32(c["q"]), _f32(c["ke"]), _f32(c["ve"]), _f32(c["kp"]), _f32(c["vp"]),
                                  c["qo"], c["kv"], c["idx"], 0.125, window=16, q_positions=c["qpos"],
                                  kv_positions=c["kpos"])
+    assert np.abs(_f32(out) - want).max() <= TOL
+
+
+@pytest.mark.parametrize("d,idx_dtype", [(64, torch.int32), (128, torch.int64)])
+def test_strided_pool_and_extend_views(device, d, idx_dtype):
+    """K/V pools and extend rows that are views into wider buffers (slot and
+    token strides beyond one row): the tile loads address rows by stride."""
+    hq, hkv, extra = 16, 2, 3
+    c = _case(device, hq, hkv, d, [40, 17], [130, 64], seed=5)
+    g = torch.Generator().manual_seed(6)
+    dv = c["dev"]
+
+    def widen(t):
+        big = torch.randn((t.shape[0], t.shape[1] + extra, d), generator=g).to(torch.bfloat16).to(device)
+        big[:, 1 : 1 + t.shape[1]] = t
+        return big[:, 1 : 1 + t.shape[1]]
+
+    kp, vp, ke, ve = widen(dv["kp"]), widen(dv["vp"]), widen(dv["ke"]), widen(dv["ve"])
+    assert not kp.is_contiguous() and kp.stride(0) == (hkv + extra) * d
+    qo = torch.from_numpy(c["qo"]).to(device)
+    kv = torch.from_numpy(c["kv"]).to(device)
+    idx = torch.from_numpy(c["idx"]).to(idx_dtype).to(device)
+    out = torch.empty(dv["q"].shape, dtype=torch.float32, device=device)
+    ca.extend_attention_fwd(dv["q"], ke, ve, out, kp, vp, qo, kv, idx, None, True, None, 40, sm_scale=d ** -0.5,
+                            sliding_window_size=-1)
+    torch.cuda.synchronize()
+    want = oat.context_attention(_f32(c["q"]), _f32(c["ke"]), _f32(c["ve"]), _f32(c["kp"]), _f32(c["vp"]),
+                                 c["qo"], c["kv"], c["idx"], d ** -0.5)
     assert np.abs(_f32(out) - want).max() <= TOL
 
 
