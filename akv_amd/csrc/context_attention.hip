@@ -129,11 +129,15 @@ __device__ __forceinline__ u32x4 load16b(const char* p) {
   return *((const global_u32x4*)p);
 }
 
+// One of the two LDS tile buffers.  They are separate objects, named
+// statically in each half of the unrolled tile loop, so the compiler sees
+// that this tile's LDS reads never touch the other buffer that the next
+// tile's direct loads are filling (no wait on those loads mid-tile).
 template <int D>
-struct Smem {
-  __bf16 k[2][kKeys][D];   // key-major K tile, 16 B chunks swizzled per row (swz_k)
-  __bf16 v[2][kKeys][D];   // key-major V tile, read transposed (ds_read_b64_tr_b16), swizzled (swz_v)
-  int32_t pos[2][kKeys];   // key positions relative to the block's first query
+struct TileLds {
+  __bf16 k[kKeys][D];   // key-major K tile, 16 B chunks swizzled per row (swz_k)
+  __bf16 v[kKeys][D];   // key-major V tile, read transposed (ds_read_b64_tr_b16), swizzled (swz_v)
+  int32_t pos[kKeys];   // key positions relative to the block's first query
 };
 
 // Chunk swizzles: logical 16 B chunk c of row r lives at chunk c ^ swz(r).
@@ -162,7 +166,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   constexpr int kChunks = D / 8;               // 16 B chunks per key row
   constexpr int kKSteps = D / 32;              // MFMA k-steps over head dims
   constexpr int kDTiles = D / 16;              // O^T row tiles
-  __shared__ __attribute__((aligned(16))) Smem<D> sm;
+  __shared__ __attribute__((aligned(16))) TileLds<D> tile0, tile1;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -277,7 +281,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
       slot[u] = static_cast<SlotT>(slots[j < plen ? j : plen - 1]);
     }
   };
-  auto stage = [&](int it, int buf) {
+  auto stage = [&](int it, TileLds<D>& t) {
     // branch-free: keys past the end read the last valid row (masked out later)
     const bool ext = it >= n_pref;
     const int32_t base = tile_base(it);
@@ -300,8 +304,8 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
         krow = reinterpret_cast<const char*>(kpool + slot[u] * a.kp_ss);
         vrow = reinterpret_cast<const char*>(vpool + slot[u] * a.vp_ss);
       }
-      __builtin_amdgcn_global_load_lds(krow + 16 * ck, (lds_void*)(&sm.k[buf][blk * kRowsPerBlock][0]), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vrow + 16 * cv, (lds_void*)(&sm.v[buf][blk * kRowsPerBlock][0]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(krow + 16 * ck, (lds_void*)(&t.k[blk * kRowsPerBlock][0]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vrow + 16 * cv, (lds_void*)(&t.v[blk * kRowsPerBlock][0]), 16, 0, 0);
     }
     if (tid < kKeys) {
       // loaded now, converted at commit: no wait on the tile's row loads here
@@ -314,8 +318,8 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   };
   // positions of the staged tile, then wait for its direct loads (vmcnt) so
   // the barrier that follows publishes the whole tile
-  auto commit = [&](int buf) {
-    if (tid < kKeys) sm.pos[buf][tid] = pvalid ? rel_pos(preg, qbase) : kFar;
+  auto commit = [&](TileLds<D>& t) {
+    if (tid < kKeys) t.pos[tid] = pvalid ? rel_pos(preg, qbase) : kFar;
     __builtin_amdgcn_s_waitcnt(0);
   };
 
@@ -334,14 +338,14 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
                         __bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f)};
 
   if (n_pref > 0) fetch_slots(0);
-  stage(0, 0);
+  stage(0, tile0);
   if (1 < n_pref) fetch_slots(1);
-  commit(0);
+  commit(tile0);
   __syncthreads();
-  for (int it = 0; it < n_tiles; ++it) {
-    const int buf = it & 1;
+  // tile it from cur while tile it + 1 streams into nxt
+  auto step = [&](int it, TileLds<D>& cur, TileLds<D>& nxt) {
     if (it + 1 < n_tiles) {
-      stage(it + 1, buf ^ 1);
+      stage(it + 1, nxt);
       if (it + 2 < n_pref) fetch_slots(it + 2);
     }
     const bool ext = it >= n_pref;
@@ -350,7 +354,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
     const int count = left < kKeys ? left : kKeys;
     // masking is needed for a partial tile, keys past the block's first
     // query (causal), or keys older than the last query's window
-    const int32_t pos0 = __builtin_amdgcn_readfirstlane(sm.pos[buf][0]);
+    const int32_t pos0 = __builtin_amdgcn_readfirstlane(cur.pos[0]);
     const bool masked = count < kKeys || (ext && base + kKeys - 1 > t0) ||
                         (a.window >= 0 && pos0 < last_rel - a.window);
 
@@ -364,7 +368,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
       for (int ks = 0; ks < kKSteps; ++ks) {
         const int krow = 16 * kt + col;
         const bf16x8 kop = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const u32x4*>(&sm.k[buf][krow][8 * ((4 * ks + quad) ^ swz_k<D>(krow))]));
+            bf16x8, *reinterpret_cast<const u32x4*>(&cur.k[krow][8 * ((4 * ks + quad) ^ swz_k<D>(krow))]));
 #pragma unroll
         for (int s = 0; s < kSub; ++s)
           sacc[kt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[s][ks], sacc[kt][s], 0, 0, 0);
@@ -391,7 +395,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
           const int32_t thr = a.window >= 0 ? row_rel[s] - a.window : -kFar - 1;
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt) {
-            const i32x4 kp = *reinterpret_cast<const i32x4*>(&sm.pos[buf][16 * kt + 4 * quad]);
+            const i32x4 kp = *reinterpret_cast<const i32x4*>(&cur.pos[16 * kt + 4 * quad]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const bool vis = (16 * kt + 4 * quad + i <= last) & (kp[i] >= thr);
@@ -446,9 +450,9 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
         const int vr0 = 32 * kk + 4 * quad + (col >> 2), vr1 = vr0 + 16;
         const int vc = 2 * dt + ((col & 3) >> 1), vh = 4 * (col & 1);
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)&sm.v[buf][vr0][8 * (vc ^ swz_v<D>(vr0)) + vh]);
+            (lds_s16x4*)&cur.v[vr0][8 * (vc ^ swz_v<D>(vr0)) + vh]);
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)&sm.v[buf][vr1][8 * (vc ^ swz_v<D>(vr1)) + vh]);
+            (lds_s16x4*)&cur.v[vr1][8 * (vc ^ swz_v<D>(vr1)) + vh]);
         const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int s = 0; s < kSub; ++s)
@@ -462,8 +466,12 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
       for (int s = 0; s < kSub; ++s)
         lacc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kOnes, pop[s][kk], lacc[s], 0, 0, 0);
 
-    if (it + 1 < n_tiles) commit(buf ^ 1);
+    if (it + 1 < n_tiles) commit(nxt);
     __syncthreads();
+  };
+  for (int it = 0; it < n_tiles; it += 2) {
+    step(it, tile0, tile1);
+    if (it + 1 < n_tiles) step(it + 1, tile1, tile0);
   }
 
   // normalise with the sink; store
