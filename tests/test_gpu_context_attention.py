@@ -135,6 +135,20 @@ def test_strided_pool_and_extend_views(device, d, idx_dtype):
     assert np.abs(_f32(out) - want).max() <= TOL
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 4), (32, 2), (64, 2)])
+def test_group_sizes(device, d, hq, hkv):
+    """GQA groups of 1, 2, 16 and 32 q heads per KV head: a block holds
+    rows_per_block / group tokens (256 down to 4), with causal, prefix,
+    window and sink handling unchanged."""
+    c = _case(device, hq, hkv, d, [3, 70, 300], [0, 45, 200], seed=hq + d)
+    sinks = (torch.randn(hq, generator=torch.Generator().manual_seed(3))).to(device)
+    got, want = _run(device, c, window=32, positions=True, sinks=sinks, out_dtype=torch.float32, scale=d ** -0.5)
+    assert np.abs(got - want).max() <= TOL
+    got, want = _run(device, c, window=-1, positions=False, sinks=None, out_dtype=torch.bfloat16, scale=d ** -0.5)
+    assert np.abs(got - want).max() <= TOL
+
+
 def test_metadata_path_ordinary_sequences(device):
     """ContextSequence.ordinary -> ContextAttentionPlan.merge/bind -> forward."""
     hq, hkv, d = 64, 8, 64
