@@ -170,7 +170,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS block bases in SGPRs
   const int col = lane & 15;
   const int quad = lane >> 4;
   const int seg = blockIdx.z;
