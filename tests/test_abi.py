@@ -62,6 +62,16 @@ def test_validation_rejects_before_any_device_work(lib):
     assert lib.akv_bind_workspace_bytes(4, 100000) > 0
     assert lib.akv_context_attention(*zeros(lib.akv_context_attention, a15=1, a17=1, a18=64, a34=4)) == _lib.AKV_EINVAL
     assert lib.akv_window_count(*zeros(lib.akv_window_count)) == _lib.AKV_EINVAL
+    assert lib.akv_window_compile_bounded(*zeros(lib.akv_window_compile_bounded)) == _lib.AKV_EINVAL
+    assert "null host pointer" in _lib.last_error()
+    # every pointer present, a negative capacity: rejected before any replay
+    one = np.zeros(8, dtype=np.int32)
+    caps = np.array([4, 1, -1], dtype=np.int64)
+    counts = np.zeros(4, dtype=np.int64)
+    p32 = one.ctypes.data
+    assert lib.akv_window_compile_bounded(1, p32, p32, p32, 0, p32, p32, p32, p32, p32, 0, 1, caps.ctypes.data,
+                                          counts.ctypes.data, *([p32] * 7)) == _lib.AKV_EINVAL
+    assert "negative capacity" in _lib.last_error()
     assert lib.akv_decode_attention(*zeros(lib.akv_decode_attention, a9=1, a11=1, a12=64)) == _lib.AKV_EINVAL
     assert "q heads" in _lib.last_error()
     ws = lib.akv_compact_workspace_bytes(64, 65536)
