@@ -16,7 +16,9 @@
 // context window are ordered), which lets a workgroup start the prefix and
 // extend loops at the first key inside the window.
 //
-// Workgroup = (block of R / G query tokens, KV head g, segment), with the
+// Workgroup = (block of R / G query tokens, KV head g, segment), KV head
+// fastest in the grid (workgroup id mod 8 picks the XCD: with 8 KV heads each
+// XCD's L2 serves one head's K/V), with the
 // G q heads of the group packed as rows: row r = token * G + head; R = 256
 // rows at head_dim 64 (4 waves x 64 rows, so each wave's reads of a K/V tile
 // from LDS feed 64 rows), 128 at head_dim 128 (4 waves x 32 rows).  Per
@@ -85,7 +87,7 @@ struct CtxArgs {
   int32_t window;
   float scale_log2;
   int32_t out_f32;
-  int32_t group, tokens_per_block;
+  int32_t group, tokens_per_block, kv_heads;
 };
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -174,13 +176,15 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   const int col = lane & 15;
   const int quad = lane >> 4;
   const int seg = blockIdx.z;
-  const int g = blockIdx.y;
   const bool i64 = a.indptr_i64;
   const int64_t qo0 = load_index(a.qo_indptr, i64, seg);
   const int32_t qlen = static_cast<int32_t>(load_index(a.qo_indptr, i64, seg + 1) - qo0);
   const int G = a.group;
   const int T = a.tokens_per_block;
-  const int32_t t0 = static_cast<int32_t>(blockIdx.x) * T;
+  // KV head fastest: workgroup id mod 8 picks the XCD, so with 8 KV heads
+  // every XCD streams one head's K/V through its own L2
+  const int g = static_cast<int>(blockIdx.x % static_cast<unsigned>(a.kv_heads));
+  const int32_t t0 = static_cast<int32_t>(blockIdx.x / static_cast<unsigned>(a.kv_heads)) * T;
   if (t0 >= qlen) return;
   const int64_t kv0 = load_index(a.kv_indptr, i64, seg);
   // without prefix indices there is no prefix, whatever kv_indptr says
@@ -613,8 +617,9 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
   a.group = q_heads / kv_heads;
   a.tokens_per_block = rows_per_block(head_dim) / a.group;
   const int64_t blocks = (max_query_len + a.tokens_per_block - 1) / a.tokens_per_block;
-  if (blocks > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_context_attention: queries too long");
-  const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(kv_heads), static_cast<unsigned>(n_segments));
+  if (blocks * kv_heads > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_context_attention: queries too long");
+  a.kv_heads = kv_heads;
+  const dim3 grid(static_cast<unsigned>(blocks * kv_heads), 1u, static_cast<unsigned>(n_segments));
   hipStream_t st = as_stream(stream);
   const bool idx64 = indices_dtype == AKV_I64;
   const int pos = q_positions == nullptr ? 0 : (positions_dtype == AKV_I64 ? 2 : 1);
