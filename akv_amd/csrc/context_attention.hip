@@ -182,9 +182,12 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   const int G = a.group;
   const int T = a.tokens_per_block;
   // KV head fastest: workgroup id mod 8 picks the XCD, so with 8 KV heads
-  // every XCD streams one head's K/V through its own L2
+  // every XCD streams one head's K/V through its own L2.  Token blocks run
+  // last-first: the last blocks see the most causal keys, and starting them
+  // first shortens the tail of the launch.
   const int g = static_cast<int>(blockIdx.x % static_cast<unsigned>(a.kv_heads));
-  const int32_t t0 = static_cast<int32_t>(blockIdx.x / static_cast<unsigned>(a.kv_heads)) * T;
+  const int32_t t0 = static_cast<int32_t>(gridDim.x / static_cast<unsigned>(a.kv_heads) - 1 -
+                                          blockIdx.x / static_cast<unsigned>(a.kv_heads)) * T;
   if (t0 >= qlen) return;
   const int64_t kv0 = load_index(a.kv_indptr, i64, seg);
   // without prefix indices there is no prefix, whatever kv_indptr says
