@@ -335,9 +335,13 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   for (int dt = 0; dt < kDTiles; ++dt)
 #pragma unroll
     for (int s = 0; s < kSub; ++s) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[kSub];
+  // per row: the reference maximum m_run (log2 domain), its negation as the
+  // exp2 shift (0 while the row has seen no key), and the raw-score level
+  // above which a tile moves it, (m_run + kLazy) / scale -- all three change
+  // only when the maximum moves
+  float m_run[kSub], neg_m[kSub], bump_at[kSub];
 #pragma unroll
-  for (int s = 0; s < kSub; ++s) m_run[s] = -INFINITY;
+  for (int s = 0; s < kSub; ++s) m_run[s] = -INFINITY, neg_m[s] = 0.f, bump_at[s] = -INFINITY;
   f32x4 lacc[kSub];  // row sums (4 equal copies)
 #pragma unroll
   for (int s = 0; s < kSub; ++s) lacc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -418,25 +422,26 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
         const float m4 = max3(t[3][0], t[3][1], t[3][2]);
         float mx = max3(max3(m0, m1, m2), max3(m3, m4, t[3][3]), -INFINITY);
         mx = row_max(mx);
-        const float tmax = mx * a.scale_log2;  // -inf when the row sees nothing here
-        const bool bump = tmax > m_run[s] + kLazy;
+        // mx = -inf when the row sees nothing here (never above bump_at)
+        const bool bump = mx > bump_at[s];
         if (__builtin_amdgcn_ballot_w64(bump)) {
-          const float m_new = bump ? tmax : m_run[s];
+          const float m_new = bump ? mx * a.scale_log2 : m_run[s];
           const float alpha = bump ? __builtin_amdgcn_exp2f(m_run[s] - m_new) : 1.f;  // m_run = -inf -> 0
           lacc[s] *= alpha;
 #pragma unroll
           for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] *= alpha;
           m_run[s] = m_new;
+          // a row that has seen no key yet has only -inf scores: any finite shift
+          neg_m[s] = m_new == -INFINITY ? 0.f : -m_new;
+          bump_at[s] = (m_new + kLazy) / a.scale_log2;
         }
-        // a row that has seen no key yet has only -inf scores: any finite shift
-        const float neg_m = m_run[s] == -INFINITY ? 0.f : -m_run[s];
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           f32x4 e0, e1;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            e0[i] = __builtin_amdgcn_exp2f(fmaf(t[2 * kk][i], a.scale_log2, neg_m));
-            e1[i] = __builtin_amdgcn_exp2f(fmaf(t[2 * kk + 1][i], a.scale_log2, neg_m));
+            e0[i] = __builtin_amdgcn_exp2f(fmaf(t[2 * kk][i], a.scale_log2, neg_m[s]));
+            e1[i] = __builtin_amdgcn_exp2f(fmaf(t[2 * kk + 1][i], a.scale_log2, neg_m[s]));
           }
           const bf16x4 b0 = __builtin_convertvector(e0, bf16x4);
           const bf16x4 b1 = __builtin_convertvector(e1, bf16x4);
