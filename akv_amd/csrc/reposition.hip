@@ -10,8 +10,8 @@
 //
 // MI355X design (not the reference's one-program-per-(token, layer, head)
 // grid): one workgroup per moved token walks every layer of the group, so the
-// token's slots, positions and its cos/sin rows are read once and kept in
-// registers (and cos^2 + sin^2 computed once) instead of once per
+// token's slots and positions are read once and its cos/sin rows (with
+// cos^2 + sin^2) are staged once in LDS instead of being reloaded for every
 // (layer, head).  Each lane owns one "rotary unit" of a head: for NeoX style
 // the 16-byte chunk at i and its partner chunk at i + R/2, so both halves of
 // every pair sit in the same lane and no cross-lane exchange is needed; for
@@ -20,8 +20,6 @@
 // instruction for the 8 x 64 bf16 head layout.  Layers whose base address is
 // not 16-byte aligned take an element-wise path inside the same kernel; other
 // shapes go to a generic element-per-thread kernel.
-#include <cstdlib>
-
 #include "common.h"
 
 namespace akv {
@@ -88,68 +86,44 @@ __device__ __forceinline__ __bf16 from_float<__bf16>(float x) {
   return static_cast<__bf16>(x);
 }
 
-// 16 bytes of storage <-> fp32 values.
+// Elements e and e + 1 (e even) of a 16-byte unit held as four 32-bit words,
+// to fp32 and back.  For 16-bit types the pair is one word; for fp32 two.
 template <typename T>
-__device__ __forceinline__ void unpack(const u32x4 u, float (&f)[Elem<T>::kVec]);
-
+__device__ __forceinline__ void unpack_two(const uint32_t (&w)[4], int e, float* f);
 template <>
-__device__ __forceinline__ void unpack<__bf16>(const u32x4 u, float (&f)[8]) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    f[2 * k] = __uint_as_float(w[k] << 16);
-    f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
-  }
+__device__ __forceinline__ void unpack_two<__bf16>(const uint32_t (&w)[4], int e, float* f) {
+  const uint32_t x = w[e >> 1];
+  f[0] = __uint_as_float(x << 16);
+  f[1] = __uint_as_float(x & 0xffff0000u);
 }
-
 template <>
-__device__ __forceinline__ void unpack<_Float16>(const u32x4 u, float (&f)[8]) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const f16x2_t h = __builtin_bit_cast(f16x2_t, w[k]);
-    f[2 * k] = static_cast<float>(h.x);
-    f[2 * k + 1] = static_cast<float>(h.y);
-  }
+__device__ __forceinline__ void unpack_two<_Float16>(const uint32_t (&w)[4], int e, float* f) {
+  const f16x2_t h = __builtin_bit_cast(f16x2_t, w[e >> 1]);
+  f[0] = static_cast<float>(h.x);
+  f[1] = static_cast<float>(h.y);
 }
-
 template <>
-__device__ __forceinline__ void unpack<float>(const u32x4 u, float (&f)[4]) {
-  f[0] = __uint_as_float(u.x);
-  f[1] = __uint_as_float(u.y);
-  f[2] = __uint_as_float(u.z);
-  f[3] = __uint_as_float(u.w);
+__device__ __forceinline__ void unpack_two<float>(const uint32_t (&w)[4], int e, float* f) {
+  f[0] = __uint_as_float(w[e]);
+  f[1] = __uint_as_float(w[e + 1]);
 }
 
 template <typename T>
-__device__ __forceinline__ u32x4 pack(const float (&f)[Elem<T>::kVec]);
-
+__device__ __forceinline__ void pack_two(const float* f, int e, uint32_t (&w)[4]);
 template <>
-__device__ __forceinline__ u32x4 pack<__bf16>(const float (&f)[8]) {
-  uint32_t w[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const f32x2_t v = {f[2 * k], f[2 * k + 1]};
-    w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-  }
-  return make_u32x4(w[0], w[1], w[2], w[3]);
+__device__ __forceinline__ void pack_two<__bf16>(const float* f, int e, uint32_t (&w)[4]) {
+  const f32x2_t v = {f[0], f[1]};
+  w[e >> 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
-
 template <>
-__device__ __forceinline__ u32x4 pack<_Float16>(const float (&f)[8]) {
-  uint32_t w[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const f32x2_t v = {f[2 * k], f[2 * k + 1]};
-    w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
-  }
-  return make_u32x4(w[0], w[1], w[2], w[3]);
+__device__ __forceinline__ void pack_two<_Float16>(const float* f, int e, uint32_t (&w)[4]) {
+  const f32x2_t v = {f[0], f[1]};
+  w[e >> 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
 }
-
 template <>
-__device__ __forceinline__ u32x4 pack<float>(const float (&f)[4]) {
-  return make_u32x4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
-                    __float_as_uint(f[3]));
+__device__ __forceinline__ void pack_two<float>(const float* f, int e, uint32_t (&w)[4]) {
+  w[e] = __float_as_uint(f[0]);
+  w[e + 1] = __float_as_uint(f[1]);
 }
 
 // KV rows live in global memory; the layer pointers arrive as plain 64-bit
@@ -157,16 +131,12 @@ __device__ __forceinline__ u32x4 pack<float>(const float (&f)[4]) {
 // instructions.
 typedef __attribute__((address_space(1))) u32x4 global_u32x4;
 
-// 16-byte load/store; `aligned` is wave-uniform.  Plain (temporal) accesses:
-// on MI355X they measured faster than the nontemporal forms for this
-// scattered 1 KiB-row pattern (AKV_REPOSITION_NT selects the latter).
-template <typename T>
-__device__ __forceinline__ u32x4 load16(const T* p, bool aligned) {
-#ifdef AKV_REPOSITION_NT
-  if (aligned) return __builtin_nontemporal_load((const global_u32x4*)(p));
-#else
-  if (aligned) return *((const global_u32x4*)(p));
-#endif
+// 16-byte load/store; ALIGNED is decided once per workgroup.  Plain
+// (temporal) accesses: on MI355X they measured faster than the nontemporal
+// forms for this scattered 1 KiB-row pattern.
+template <bool ALIGNED, typename T>
+__device__ __forceinline__ u32x4 load16(const T* p) {
+  if (ALIGNED) return *((const global_u32x4*)(p));
   union {
     u32x4 u;
     T e[Elem<T>::kVec];
@@ -176,14 +146,10 @@ __device__ __forceinline__ u32x4 load16(const T* p, bool aligned) {
   return r.u;
 }
 
-template <typename T>
-__device__ __forceinline__ void store16(T* p, u32x4 v, bool aligned) {
-  if (aligned) {
-#ifdef AKV_REPOSITION_NT
-    __builtin_nontemporal_store(v, (global_u32x4*)(p));
-#else
+template <bool ALIGNED, typename T>
+__device__ __forceinline__ void store16(T* p, u32x4 v) {
+  if (ALIGNED) {
     *((global_u32x4*)(p)) = v;
-#endif
     return;
   }
   union {
@@ -195,16 +161,12 @@ __device__ __forceinline__ void store16(T* p, u32x4 v, bool aligned) {
   for (int k = 0; k < Elem<T>::kVec; ++k) p[k] = r.e[k];
 }
 
-// Loads NP consecutive table values as fp32.  The host guarantees that the
-// table base, its row stride and every unit offset are multiples of the
-// vector size.
-template <typename CS, int NP>
-__device__ __forceinline__ void load_table(const CS* p, float (&out)[NP]) {
-  typedef CS vec_t __attribute__((ext_vector_type(NP)));
-  const vec_t v = *reinterpret_cast<const vec_t*>(p);
-#pragma unroll
-  for (int k = 0; k < NP; ++k) out[k] = to_float(v[k]);
-}
+// Floats between the coefficient arrays of one token in LDS: `half`
+// rounded up to 8 so every array starts 32-byte aligned.
+__host__ __device__ __forceinline__ int coef_stride(int half) { return (half + 7) & ~7; }
+
+// Two coefficients from LDS.
+__device__ __forceinline__ float2 lds2(const float* p) { return *reinterpret_cast<const float2*>(p); }
 
 // The reference rotation, op for op (context_reposition.py:92-102).
 __device__ __forceinline__ void rotate(float x1, float x2, float co, float so, float s,
@@ -219,99 +181,136 @@ __device__ __forceinline__ void rotate(float x1, float x2, float co, float so, f
 struct RowData {
   u32x4 k1, k2;  // rotary unit of K (the partner half for NeoX style)
   u32x4 v[2];    // this lane's first two V units
-  uintptr_t kb, vb;
-  bool aligned;
+  char* kb;      // the layer's K and V base addresses
+  char* vb;
 };
 
-template <typename T, typename CS, bool NEOX>
+// WIDE: the row has a K tail (rotary_dim < head_dim) or more V units than
+// two per lane; the host picks it, so the common full-rotary shapes carry no
+// tail loops.
+template <typename T, typename CS, bool NEOX, bool WIDE>
 struct RowMover {
   static constexpr int VEC = Elem<T>::kVec;
   static constexpr int NP = NEOX ? VEC : VEC / 2;  // rotation pairs per lane
   const RepositionArgs& a;
-  int64_t src, dst;
-  int h, j, off1, off2, lpr, v_units_head, v_units_row, t_units_head, t_units_row;
+  // byte offsets of the token's source and destination slot rows
+  int64_t k_src, k_dst, v_src, v_dst;
+  // byte offsets inside a slot row (the host keeps a row's span below 2^31):
+  // this lane's K unit and its NeoX partner, and its first two V units
+  int32_t ko1, ko2, vo0, vo1;
+  bool has_v0, has_v1;
+  int j, lpr;
   bool same;
-  float co[NP], so[NP], cn[NP], sn[NP], s2[NP];
+  // this lane's first frequency in the token's LDS block of five arrays
+  // (cos old, sin old, cos new, sin new, cos^2 + sin^2 of old), each `cstride`
+  // floats apart
+  const float* coef;
+  int cstride;
 
+  __device__ __forceinline__ const T* at(const char* base, int64_t row, int32_t off) const {
+    return reinterpret_cast<const T*>(base + row + off);
+  }
+  __device__ __forceinline__ T* at(char* base, int64_t row, int32_t off) const {
+    return reinterpret_cast<T*>(base + row + off);
+  }
+
+  template <bool ALIGNED>
   __device__ __forceinline__ RowData load(int layer) const {
     RowData r;
-    r.kb = static_cast<uintptr_t>(a.k_ptrs[layer]);
-    r.vb = static_cast<uintptr_t>(a.v_ptrs[layer]);
-    // one wave may hold rows of several layers: take the vector path only
-    // when every row of the wave is 16-byte aligned (a uniform branch)
-    r.aligned = __ballot(((r.kb | r.vb) & 15) != 0) == 0;
-    const T* ks = reinterpret_cast<const T*>(r.kb) + src * a.k_stride_slot + h * a.k_stride_head;
-    r.k1 = load16(ks + off1, r.aligned);
-    r.k2 = NEOX ? load16(ks + off2, r.aligned) : make_u32x4(0, 0, 0, 0);
-    const T* vs = reinterpret_cast<const T*>(r.vb) + src * a.v_stride_slot;
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int c = j + q * lpr;
-      if (c < v_units_row) {
-        const int vh = c / v_units_head;
-        r.v[q] = load16(vs + vh * a.v_stride_head + (c - vh * v_units_head) * VEC, r.aligned);
-      }
-    }
+    r.kb = reinterpret_cast<char*>(static_cast<uintptr_t>(a.k_ptrs[layer]));
+    r.vb = reinterpret_cast<char*>(static_cast<uintptr_t>(a.v_ptrs[layer]));
+    r.k1 = load16<ALIGNED>(at(r.kb, k_src, ko1));
+    r.k2 = NEOX ? load16<ALIGNED>(at(r.kb, k_src, ko2)) : make_u32x4(0, 0, 0, 0);
+    if (has_v0) r.v[0] = load16<ALIGNED>(at(r.vb, v_src, vo0));
+    if (has_v1) r.v[1] = load16<ALIGNED>(at(r.vb, v_src, vo1));
     return r;
   }
 
+  template <bool ALIGNED>
   __device__ __forceinline__ void finish(const RowData& r) const {
-    T* kb = reinterpret_cast<T*>(r.kb);
-    T* vb = reinterpret_cast<T*>(r.vb);
-    T* kd = kb + dst * a.k_stride_slot + h * a.k_stride_head;
+    // V first: it needs no arithmetic, and its registers free up before the
+    // rotation's
+    if (has_v0) store16<ALIGNED>(at(r.vb, v_dst, vo0), r.v[0]);
+    if (has_v1) store16<ALIGNED>(at(r.vb, v_dst, vo1), r.v[1]);
     u32x4 o1 = r.k1, o2 = r.k2;
     if (!same) {
-      float x1[VEC], x2[VEC], y1[VEC], y2[VEC];
-      unpack<T>(r.k1, x1);
-      if (NEOX) {
-        unpack<T>(r.k2, x2);
+      // two pairs at a time: their ten coefficients are read from LDS just
+      // before use, so few registers stay live
+      const uint32_t w1[4] = {o1.x, o1.y, o1.z, o1.w};
+      const uint32_t w2[4] = {o2.x, o2.y, o2.z, o2.w};
+      uint32_t r1[4], r2[4];
 #pragma unroll
-        for (int k = 0; k < NP; ++k) rotate(x1[k], x2[k], co[k], so[k], s2[k], cn[k], sn[k], y1[k], y2[k]);
-        o1 = pack<T>(y1);
-        o2 = pack<T>(y2);
-      } else {
-#pragma unroll
-        for (int k = 0; k < NP; ++k)
-          rotate(x1[2 * k], x1[2 * k + 1], co[k], so[k], s2[k], cn[k], sn[k], y1[2 * k], y1[2 * k + 1]);
-        o1 = pack<T>(y1);
+      for (int k = 0; k < NP; k += 2) {
+        // a scheduling fence per chunk keeps the compiler from issuing every
+        // chunk's LDS reads up front (which holds all coefficients in
+        // registers)
+        __builtin_amdgcn_sched_barrier(0);
+        const float2 co = lds2(coef + k);
+        const float2 so = lds2(coef + cstride + k);
+        const float2 cn = lds2(coef + 2 * cstride + k);
+        const float2 sn = lds2(coef + 3 * cstride + k);
+        const float2 s2 = lds2(coef + 4 * cstride + k);
+        float x1[2], x2[2], y1[2], y2[2];
+        if (NEOX) {
+          // pairs k, k+1: element k (and k+1) of each half
+          unpack_two<T>(w1, k, x1);
+          unpack_two<T>(w2, k, x2);
+        } else {
+          // pair k is elements 2k, 2k+1 of the interleaved unit
+          float e[4];
+          unpack_two<T>(w1, 2 * k, e);
+          unpack_two<T>(w1, 2 * k + 2, e + 2);
+          x1[0] = e[0];
+          x2[0] = e[1];
+          x1[1] = e[2];
+          x2[1] = e[3];
+        }
+        rotate(x1[0], x2[0], co.x, so.x, s2.x, cn.x, sn.x, y1[0], y2[0]);
+        rotate(x1[1], x2[1], co.y, so.y, s2.y, cn.y, sn.y, y1[1], y2[1]);
+        if (NEOX) {
+          pack_two<T>(y1, k, r1);
+          pack_two<T>(y2, k, r2);
+        } else {
+          const float e1[2] = {y1[0], y2[0]}, e2[2] = {y1[1], y2[1]};
+          pack_two<T>(e1, 2 * k, r1);
+          pack_two<T>(e2, 2 * k + 2, r1);
+        }
       }
+      o1 = make_u32x4(r1[0], r1[1], r1[2], r1[3]);
+      if (NEOX) o2 = make_u32x4(r2[0], r2[1], r2[2], r2[3]);
     }
-    store16(kd + off1, o1, r.aligned);
-    if (NEOX) store16(kd + off2, o2, r.aligned);
-    const T* vs = vb + src * a.v_stride_slot;
-    T* vd = vb + dst * a.v_stride_slot;
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int c = j + q * lpr;
-      if (c < v_units_row) {
-        const int vh = c / v_units_head;
-        store16(vd + vh * a.v_stride_head + (c - vh * v_units_head) * VEC, r.v[q], r.aligned);
-      }
-    }
+    store16<ALIGNED>(at(r.kb, k_dst, ko1), o1);
+    if (NEOX) store16<ALIGNED>(at(r.kb, k_dst, ko2), o2);
+    if (!WIDE) return;
     // V units beyond two per lane (wide heads with few rotary units)
+    const int v_units_head = a.head_dim / VEC;
+    const int v_units_row = a.n_heads * v_units_head;
     for (int c = j + 2 * lpr; c < v_units_row; c += lpr) {
       const int vh = c / v_units_head;
-      const int ve = (c - vh * v_units_head) * VEC;
-      store16(vd + vh * a.v_stride_head + ve, load16(vs + vh * a.v_stride_head + ve, r.aligned), r.aligned);
+      const int32_t off = static_cast<int32_t>((vh * a.v_stride_head + (c - vh * v_units_head) * VEC) * sizeof(T));
+      store16<ALIGNED>(at(r.vb, v_dst, off), load16<ALIGNED>(at(r.vb, v_src, off)));
     }
     // K tail dims [R, D)
+    const int t_units_head = (a.head_dim - a.rotary_dim) / VEC;
+    const int t_units_row = a.n_heads * t_units_head;
     for (int c = j; c < t_units_row; c += lpr) {
       const int th = c / t_units_head;
-      const int te = a.rotary_dim + (c - th * t_units_head) * VEC;
-      const T* ts = kb + src * a.k_stride_slot + th * a.k_stride_head + te;
-      T* td = kb + dst * a.k_stride_slot + th * a.k_stride_head + te;
-      store16(td, load16(ts, r.aligned), r.aligned);
+      const int32_t off =
+          static_cast<int32_t>((th * a.k_stride_head + a.rotary_dim + (c - th * t_units_head) * VEC) * sizeof(T));
+      store16<ALIGNED>(at(r.kb, k_dst, off), load16<ALIGNED>(at(r.kb, k_src, off)));
     }
   }
 };
 
 // Workgroup = tokens_per_block tokens x rows_per_block layer rows side by
-// side x lanes_per_row lanes; each lane walks the layers of its token.
-template <typename T, typename CS, bool NEOX>
+// side x lanes_per_row lanes; each lane walks the layers of its token, one
+// row per pass (load, then rotate and store).  Dynamic LDS holds, per token,
+// the five coefficient arrays of its `half` frequencies.
+template <typename T, typename CS, bool NEOX, bool WIDE>
 __global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionArgs a) {
-  using Mover = RowMover<T, CS, NEOX>;
+  using Mover = RowMover<T, CS, NEOX, WIDE>;
   constexpr int VEC = Mover::VEC;
-  constexpr int NP = Mover::NP;
+  extern __shared__ float4 coef_lds[];
   const int lpr = a.lanes_per_row;
   const int row_threads = lpr * a.rows_per_block;
   const int slot = threadIdx.x / row_threads;
@@ -319,49 +318,75 @@ __global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionAr
   const int row_sub = local / lpr;
   const int j = local - row_sub * lpr;
   const int64_t token = static_cast<int64_t>(blockIdx.x) * a.tokens_per_block + slot;
-  if (slot >= a.tokens_per_block || token >= a.n_tokens) return;
-
-  Mover mv{a};
-  mv.src = a.src[token];
-  mv.dst = a.dst[token];
-  if (a.skip_unmapped && (mv.src <= 0 || mv.dst <= 0)) return;
-  const int32_t* pair = a.pairs + token * a.pair_stride;
-  const int64_t old_pos = pair[0];
-  const int64_t new_pos = pair[1];
-  mv.same = old_pos == new_pos;
   const int half = a.rotary_dim >> 1;
+  const int cstride = coef_stride(half);
+  float* coef = reinterpret_cast<float*>(coef_lds) + slot * 5 * cstride;
+
+  // every thread reaches the barrier below: a token past the end or an
+  // unmapped one only skips its work
+  Mover mv{a};
+  bool live = token < a.n_tokens;
+  int64_t src = 0, dst = 0, old_pos = 0, new_pos = 0;
+  if (live) {
+    src = a.src[token];
+    dst = a.dst[token];
+    live = !(a.skip_unmapped && (src <= 0 || dst <= 0));
+    const int32_t* pair = a.pairs + token * a.pair_stride;
+    old_pos = pair[0];
+    new_pos = pair[1];
+  }
+  mv.same = old_pos == new_pos;
+  if (live && !mv.same) {
+    const CS* table = static_cast<const CS*>(a.cos_sin);
+    const CS* ro = table + old_pos * a.rope_stride;
+    const CS* rn = table + new_pos * a.rope_stride;
+    for (int f = local; f < half; f += row_threads) {
+      const float co = to_float(ro[f]);
+      const float so = to_float(ro[half + f]);
+      coef[f] = co;
+      coef[cstride + f] = so;
+      coef[2 * cstride + f] = to_float(rn[f]);
+      coef[3 * cstride + f] = to_float(rn[half + f]);
+      coef[4 * cstride + f] = co * co + so * so;
+    }
+  }
+  // one 16-byte-unaligned layer base sends the whole workgroup down the
+  // element-wise path (a uniform branch); the flag rides on the barrier
+  bool misaligned = false;
+  for (int l = threadIdx.x; l < a.n_layers; l += blockDim.x)
+    misaligned |= ((a.k_ptrs[l] | a.v_ptrs[l]) & 15) != 0;
+  const bool aligned = !__syncthreads_or(misaligned);
+  if (!live || row_sub >= a.n_layers) return;
+
+  constexpr int64_t B = sizeof(T);
+  mv.k_src = src * a.k_stride_slot * B;
+  mv.k_dst = dst * a.k_stride_slot * B;
+  mv.v_src = src * a.v_stride_slot * B;
+  mv.v_dst = dst * a.v_stride_slot * B;
   mv.lpr = lpr;
   mv.j = j;
-  mv.h = j / a.units_per_head;
-  const int g = j - mv.h * a.units_per_head;
-  mv.off1 = g * VEC;
-  mv.off2 = NEOX ? half + g * VEC : 0;
-  const int i0 = NEOX ? g * VEC : g * (VEC / 2);
-  mv.v_units_head = a.head_dim / VEC;
-  mv.v_units_row = a.n_heads * mv.v_units_head;
-  mv.t_units_head = (a.head_dim - a.rotary_dim) / VEC;
-  mv.t_units_row = a.n_heads * mv.t_units_head;
-  if (!mv.same) {
-    const CS* table = static_cast<const CS*>(a.cos_sin);
-    load_table<CS, NP>(table + old_pos * a.rope_stride + i0, mv.co);
-    load_table<CS, NP>(table + old_pos * a.rope_stride + half + i0, mv.so);
-    load_table<CS, NP>(table + new_pos * a.rope_stride + i0, mv.cn);
-    load_table<CS, NP>(table + new_pos * a.rope_stride + half + i0, mv.sn);
-#pragma unroll
-    for (int k = 0; k < NP; ++k) mv.s2[k] = mv.co[k] * mv.co[k] + mv.so[k] * mv.so[k];
-  }
-
-  // Double-buffered over layers: the next row's loads are in flight during
-  // this row's arithmetic and stores (measured +2% over load-then-finish).
-  if (row_sub < a.n_layers) {
-    RowData cur = mv.load(row_sub);
-    for (int layer = row_sub; layer < a.n_layers; layer += a.rows_per_block) {
-      const int next = layer + a.rows_per_block;
-      RowData nxt = cur;
-      if (next < a.n_layers) nxt = mv.load(next);
-      mv.finish(cur);
-      cur = nxt;
-    }
+  const int h = j / a.units_per_head;
+  const int g = j - h * a.units_per_head;
+  mv.ko1 = static_cast<int32_t>((h * a.k_stride_head + g * VEC) * B);
+  mv.ko2 = static_cast<int32_t>((h * a.k_stride_head + half + g * VEC) * B);
+  const int v_units_head = a.head_dim / VEC;
+  const int v_units_row = a.n_heads * v_units_head;
+  const int c0 = j, c1 = j + lpr;
+  mv.has_v0 = c0 < v_units_row;
+  mv.has_v1 = c1 < v_units_row;
+  const int vh0 = c0 / v_units_head, vh1 = c1 / v_units_head;
+  mv.vo0 = static_cast<int32_t>((vh0 * a.v_stride_head + (c0 - vh0 * v_units_head) * VEC) * B);
+  mv.vo1 = static_cast<int32_t>((vh1 * a.v_stride_head + (c1 - vh1 * v_units_head) * VEC) * B);
+  mv.coef = coef + (NEOX ? g * VEC : g * (VEC / 2));
+  mv.cstride = cstride;
+  // one row in flight per lane: measured faster than prefetching the next
+  // layer's row (fewer registers, more resident waves)
+  if (aligned) {
+    for (int layer = row_sub; layer < a.n_layers; layer += a.rows_per_block)
+      mv.template finish<true>(mv.template load<true>(layer));
+  } else {
+    for (int layer = row_sub; layer < a.n_layers; layer += a.rows_per_block)
+      mv.template finish<false>(mv.template load<false>(layer));
   }
 }
 
@@ -418,30 +443,22 @@ __global__ void __launch_bounds__(256) reposition_generic_kernel(const Repositio
   }
 }
 
-int env_int(const char* name) {
-  const char* e = std::getenv(name);
-  return e ? std::atoi(e) : 0;
-}
-
 // Launch geometry of the vector kernel.  Measured on MI355X for the
-// 36-layer x 8-head x 64 bf16 shape: about 192 threads per token (6 layers
-// side by side, 6 passes each) beat both one wave per token and one row per
-// lane; tokens whose rows fill less than two waves share a workgroup.
-// AKV_REPOSITION_ROWS_PER_BLOCK / AKV_REPOSITION_TOKENS_PER_BLOCK override.
+// 36-layer x 8-head x 64 bf16 shape (32 lanes per row): about 384 threads
+// per token (12 layers side by side, 3 passes, one row in flight per lane)
+// beat 192 threads with the next layer prefetched, 576 threads, and several
+// tokens per workgroup; tokens whose rows fill less than two waves share a
+// workgroup.
 void geometry(RepositionArgs& a) {
   const int lpr = a.lanes_per_row;
-  const int forced_rows = env_int("AKV_REPOSITION_ROWS_PER_BLOCK");
-  int rows = forced_rows > 0 ? forced_rows : 192 / lpr;
+  int rows = 384 / lpr;
   if (rows < 1) rows = 1;
   if (rows > a.n_layers) rows = a.n_layers;
-  if (forced_rows <= 0) {
-    const int passes = (a.n_layers + rows - 1) / rows;
-    rows = (a.n_layers + passes - 1) / passes;  // balance the passes
-  }
+  const int passes = (a.n_layers + rows - 1) / rows;
+  rows = (a.n_layers + passes - 1) / passes;  // balance the passes
   while (rows > 1 && rows * lpr > 1024) --rows;
   a.rows_per_block = rows;
-  const int forced_tokens = env_int("AKV_REPOSITION_TOKENS_PER_BLOCK");
-  int tokens = forced_tokens > 0 ? forced_tokens : 128 / (rows * lpr);
+  int tokens = 128 / (rows * lpr);
   if (tokens < 1) tokens = 1;
   while (tokens > 1 && tokens * rows * lpr > 1024) --tokens;
   a.tokens_per_block = tokens;
@@ -457,10 +474,19 @@ int launch_typed(RepositionArgs a, int64_t n_tokens, hipStream_t stream, bool ve
     geometry(a);
     const int threads = a.lanes_per_row * a.rows_per_block * a.tokens_per_block;
     const dim3 grid(static_cast<unsigned>((n_tokens + a.tokens_per_block - 1) / a.tokens_per_block));
-    if (a.is_neox)
-      hipLaunchKernelGGL((reposition_vec_kernel<T, CS, true>), grid, dim3(threads), 0, stream, a);
-    else
-      hipLaunchKernelGGL((reposition_vec_kernel<T, CS, false>), grid, dim3(threads), 0, stream, a);
+    const size_t lds = static_cast<size_t>(a.tokens_per_block) * 5 * coef_stride(a.rotary_dim >> 1) * sizeof(float);
+    const bool wide = a.rotary_dim < a.head_dim || a.n_heads * (a.head_dim / VEC) > 2 * a.lanes_per_row;
+    if (a.is_neox) {
+      if (wide)
+        hipLaunchKernelGGL((reposition_vec_kernel<T, CS, true, true>), grid, dim3(threads), lds, stream, a);
+      else
+        hipLaunchKernelGGL((reposition_vec_kernel<T, CS, true, false>), grid, dim3(threads), lds, stream, a);
+    } else {
+      if (wide)
+        hipLaunchKernelGGL((reposition_vec_kernel<T, CS, false, true>), grid, dim3(threads), lds, stream, a);
+      else
+        hipLaunchKernelGGL((reposition_vec_kernel<T, CS, false, false>), grid, dim3(threads), lds, stream, a);
+    }
     return check_launch("akv_reposition_kv_layers");
   }
   const int64_t total = n_tokens * a.n_layers * a.n_heads * a.head_dim;
@@ -539,18 +565,19 @@ extern "C" int akv_reposition_kv_layers(const uint64_t* k_ptrs, const uint64_t* 
   a.is_neox = is_neox ? 1 : 0;
 
   // The vector kernel needs 16-byte units that never straddle a head or the
-  // rotary boundary, and a table whose per-lane slices are vector aligned.
+  // rotary boundary.
   const int vec = 16 / dtype_bytes(kv_dtype);
-  const int np = is_neox ? vec : vec / 2;
-  const int64_t cs_align = static_cast<int64_t>(np) * dtype_bytes(cos_sin_dtype);
   bool vec_ok = head_dim % vec == 0 && k_stride_slot % vec == 0 && k_stride_head % vec == 0 &&
                 v_stride_slot % vec == 0 && v_stride_head % vec == 0 &&
-                (is_neox ? rotary_dim % (2 * vec) == 0 : rotary_dim % vec == 0) &&
-                (reinterpret_cast<uintptr_t>(cos_sin) % cs_align) == 0 && rope_stride % np == 0 &&
-                ((rotary_dim / 2) % np) == 0;
+                (is_neox ? rotary_dim % (2 * vec) == 0 : rotary_dim % vec == 0);
   if (vec_ok) {
     const int units = is_neox ? rotary_dim / (2 * vec) : rotary_dim / vec;
     if (static_cast<int64_t>(n_heads) * units > 1024) vec_ok = false;
+    // byte offsets inside one slot row are 32-bit in the vector kernel
+    const int64_t row_span = (static_cast<int64_t>(n_heads) * (k_stride_head > v_stride_head ? k_stride_head
+                                                                                              : v_stride_head) +
+                              head_dim) * dtype_bytes(kv_dtype);
+    if (k_stride_head < 0 || v_stride_head < 0 || row_span >= (1LL << 31)) vec_ok = false;
   }
   hipStream_t st = as_stream(stream);
   switch (kv_dtype) {

@@ -21,14 +21,22 @@ Follows ``_reposition_layers_kernel``
 * results are narrowed with round-to-nearest-even (Triton's downcast);
 * K dims ``[R, D)`` and all of V are copied bit for bit (``:114-123``).
 
-Pinned by (``tests/test_oracle_reposition.py``): a scalar float64 evaluation
-of the same formula rounded step by step through ``numpy.float32`` on single
-elements (independent of the vectorised gather/scatter code), the identity
-``old == new`` -> bits unchanged, plain-RoPE round trips p -> q -> p within
-2 bf16 ulp, rotation by 90 degrees against the closed form (x1, x2) ->
-(-x2, x1), bitwise V/tail copies, and ``skip_unmapped`` leaving the
-destination untouched.  A dropped term, a swapped sign or a swapped cos/sin
-half fails the closed-form rotation checks.
+Pinned by (``tests/test_oracle_reposition.py``):
+
+* 64 known answers on the GPT-OSS YaRN table
+  (``tests/golden/reposition_kat.npz``) whose expected bf16 bits come from
+  exact rational arithmetic with fp32 round-to-nearest-even after every
+  operation (``tests/exact_fp.py``).  Each case was chosen so that a
+  delta-angle rotation, division of each product before the sum, and fused
+  multiply-adds all give different bits; the test plants each of those forms
+  in place of ``rotate_pairs`` and checks that the known answers reject it;
+* rotation by quarter turns (tables with cos/sin in {-m, 0, m}) against the
+  closed forms (x1, x2) -> (-x2, x1) / (x2, -x1), which catch a swapped sign,
+  a cos/sin half swap, a wrong pair index or a missing division;
+* ``old == new`` -> bits unchanged; plain-RoPE round trips p -> q -> p
+  within 2 bf16 ulp; a float64 delta rotation within 2^-6 of the pair;
+* bitwise V/tail copies, and ``skip_unmapped`` leaving the destination
+  untouched.
 
 Parity unpinned: NaN payloads.  A same-position copy here keeps the source
 bits; the reference's fp32 round trip may canonicalise a NaN's payload.  The

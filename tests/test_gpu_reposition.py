@@ -16,6 +16,7 @@ from akv_amd.rope import make_table
 from oracle import reposition as rp
 
 from helpers import ORACLE_DTYPE, single_request, storage_equal, to_storage
+from reposition_kat import kat_expected, kat_pool
 
 pytestmark = pytest.mark.gpu
 
@@ -98,9 +99,33 @@ def test_partial_rotary(device, rotary_dim):
     _run_case(device, rotary_dim=rotary_dim, neox=False, seed=4)
 
 
-@pytest.mark.parametrize("heads,head_dim,layers", [(8, 64, 36), (8, 128, 3), (4, 64, 5), (1, 16, 2), (3, 32, 2)])
+# (8, 128, 32) is the Llama-3 geometry (64 lanes per row, 3 layers side by
+# side, 11 passes with a short last pass); (4, 64, 36) one TP=2 rank's
+# GPT-OSS share (16 lanes per row, several tokens per workgroup)
+@pytest.mark.parametrize("heads,head_dim,layers", [(8, 64, 36), (8, 128, 3), (8, 128, 32), (4, 64, 36), (4, 64, 5),
+                                                   (1, 16, 2), (3, 32, 2)])
 def test_shapes(device, heads, head_dim, layers):
     _run_case(device, heads=heads, head_dim=head_dim, layers=layers, moved=64, seed=5)
+
+
+@pytest.mark.parametrize("neox", [True, False])
+def test_exact_known_answers(device, neox):
+    """The kernel against the exact-arithmetic known answers of the fp32
+    operation order (each case tells the reference order apart from a
+    delta-angle rotation, per-term division and fused multiply-adds)."""
+    k, v, src, dst, pairs, table = kat_pool(neox)
+    kt = torch.from_numpy(k[0].view(np.int16)).view(torch.bfloat16).to(device)
+    vt = torch.from_numpy(v[0].view(np.int16)).view(torch.bfloat16).to(device)
+    ptr = lambda t: torch.tensor([t.data_ptr()], dtype=torch.uint64).to(device)  # noqa: E731
+    as_i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(device)  # noqa: E731
+    ops.reposition_kv_layers(ptr(kt), ptr(vt), kt, vt, as_i32(src), as_i32(dst), as_i32(pairs),
+                             torch.from_numpy(table).to(device), is_neox_style=neox)
+    torch.cuda.synchronize()
+    got = to_storage(kt)
+    np.testing.assert_array_equal(got[dst], kat_expected("two_step", neox))
+    np.testing.assert_array_equal(to_storage(vt)[dst], v[0][src])
+    untouched = np.setdiff1d(np.arange(len(got)), dst)
+    np.testing.assert_array_equal(got[untouched], k[0][untouched])
 
 
 def test_skip_unmapped_and_same_position(device):

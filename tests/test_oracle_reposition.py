@@ -5,11 +5,15 @@ exact, so a swapped sign, a cos/sin half swap, a wrong pair index, a dropped
 division by cos^2 + sin^2 or a transposed operand gives a different answer.
 """
 
+from fractions import Fraction
+
 import numpy as np
 import pytest
 
+import exact_fp as ex
 from oracle import bf16
 from oracle import reposition as rp
+from reposition_kat import KAT, KAT_VARIANTS, kat_expected, kat_pool
 
 
 def _pool(rng, slots=8, heads=2, dim=8, layers=2, dtype="bf16"):
@@ -156,3 +160,93 @@ def test_f32_and_f16_storage():
         y = _vals(k[0][2], dtype)
         np.testing.assert_array_equal(y[:, :4], -x[:, 4:])
         np.testing.assert_array_equal(y[:, 4:], x[:, :4])
+
+
+# -- known answers for the fp32 operation order ---------------------------
+#
+# tests/golden/reposition_kat.npz holds 64 (x1, x2, old, new) cases on the
+# GPT-OSS YaRN table whose bf16 result under the reference order
+# (context_reposition.py:92-102, every operation rounded, no FMA) differs
+# from a delta-angle rotation, from dividing each product before the sum and
+# from fused multiply-adds.  The expected bits come from exact rational
+# arithmetic (tests/exact_fp.py), not from numpy.
+
+def test_kat_fixture_is_exact_and_discriminating():
+    for c in range(len(KAT["old"])):
+        args = [int(KAT[f][c]) for f in ("x1_bits", "x2_bits", "co_bits", "so_bits", "cn_bits", "sn_bits")]
+        ref = ex.rotate_bf16_bits("two_step", *args)
+        assert ref == tuple(int(b) for b in KAT["two_step_bits"][c])
+        for form in KAT_VARIANTS:
+            got = ex.rotate_bf16_bits(form, *args)
+            assert got == tuple(int(b) for b in KAT[f"{form}_bits"][c])
+            assert got != ref, (c, form)
+
+
+def test_exact_rounding_against_the_format_definition():
+    # spot checks of the rounding helper itself: ties to even, subnormals,
+    # exactly representable values, and agreement with numpy's IEEE float32
+    tie_up = Fraction(1) + Fraction(3, 2**24)  # halfway between 1+2^-23 and 1+2^-22
+    assert ex.f32(tie_up) == 1 + Fraction(2, 2**23)
+    tie_down = Fraction(1) + Fraction(1, 2**24)  # halfway between 1 and 1+2^-23
+    assert ex.f32(tie_down) == 1
+    assert ex.f32(Fraction(3, 2**150)) == Fraction(2, 2**149)  # 1.5 quanta -> 2 (even)
+    assert ex.f32(Fraction(1, 2**150)) == 0  # half the smallest subnormal -> 0 (even)
+    assert ex.round_binary(Fraction(1) + Fraction(1, 2**8), ex.BF16) == 1
+    assert ex.round_binary(Fraction(1) + Fraction(3, 2**8), ex.BF16) == 1 + Fraction(2, 2**7)
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal(200).astype(np.float32)
+    b = rng.standard_normal(200).astype(np.float32) + 2
+    for op in (np.multiply, np.add, np.subtract, np.divide):
+        got = op(a, b)
+        for i in range(len(a)):
+            x, y = Fraction(float(a[i])), Fraction(float(b[i]))
+            exact = {np.multiply: x * y, np.add: x + y, np.subtract: x - y, np.divide: x / y}[op]
+            assert ex.f32(exact) == Fraction(float(got[i]))
+
+
+@pytest.mark.parametrize("neox", [True, False])
+def test_oracle_matches_exact_operation_order(neox):
+    k, v, src, dst, pairs, table = kat_pool(neox)
+    v_before = v[0].copy()
+    rp.reposition_kv_layers(k, v, src, dst, pairs, table, dtype="bf16", is_neox_style=neox)
+    np.testing.assert_array_equal(k[0][dst], kat_expected("two_step", neox))
+    np.testing.assert_array_equal(v[0][dst], v_before[src])
+
+
+def _planted(form):
+    """numpy float32 statements of the three variants, planted in place of
+    the oracle's rotation."""
+    f = np.float32
+
+    def fma(a, b, c):
+        return (a.astype(np.float64) * b.astype(np.float64) + c.astype(np.float64)).astype(f)
+
+    def rotate(x1, x2, co, so, cn, sn):
+        x1, x2, co, so, cn, sn = (np.asarray(a, dtype=f) for a in (x1, x2, co, so, cn, sn))
+        s = co * co + so * so
+        if form == "delta_angle":
+            cd = (cn * co + sn * so) / s
+            sd = (sn * co - cn * so) / s
+            return x1 * cd - x2 * sd, x2 * cd + x1 * sd
+        if form == "per_term_division":
+            u1 = (x1 * co) / s + (x2 * so) / s
+            u2 = (x2 * co) / s - (x1 * so) / s
+            return u1 * cn - u2 * sn, u2 * cn + u1 * sn
+        s = fma(co, co, so * so)
+        u1 = fma(x1, co, x2 * so) / s
+        u2 = fma(x2, co, -(x1 * so)) / s
+        return fma(u1, cn, -(u2 * sn)), fma(u2, cn, u1 * sn)
+
+    return rotate
+
+
+@pytest.mark.parametrize("form", KAT_VARIANTS)
+def test_known_answers_reject_planted_variants(form, monkeypatch):
+    monkeypatch.setattr(rp, "rotate_pairs", _planted(form))
+    k, v, src, dst, pairs, table = kat_pool(True)
+    rp.reposition_kv_layers(k, v, src, dst, pairs, table, dtype="bf16")
+    got = k[0][dst]
+    assert not np.array_equal(got, kat_expected("two_step"))
+    # the planted form reproduces its own exact known answers on most cases
+    # (the float64 emulation of an FMA can double-round)
+    assert np.mean(np.all(got == kat_expected(form), axis=(1, 2))) > 0.9
