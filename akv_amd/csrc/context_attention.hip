@@ -575,6 +575,9 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
     return fail(AKV_EINVAL, "akv_context_attention: output must be bf16 or f32");
   if (!q || !k_ext || !v_ext || !out || !qo_indptr || !kv_indptr)
     return fail(AKV_EINVAL, "akv_context_attention: null device pointer");
+  // prefix keys are read from the pools through kv_indices
+  if (kv_indices && (!k_buffer || !v_buffer))
+    return fail(AKV_EINVAL, "akv_context_attention: prefix indices given without K/V pools");
   if ((q_positions == nullptr) != (kv_positions == nullptr))
     return fail(AKV_EINVAL, "akv_context_attention: needs both query and KV positions or neither");
   const int64_t strides[] = {q_stride_t,    q_stride_h,    k_ext_stride_t, k_ext_stride_h, v_ext_stride_t,
@@ -619,7 +622,9 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
   a.o_st = static_cast<int32_t>(out_stride_t);
   a.o_sh = static_cast<int32_t>(out_stride_h);
   a.indptr_i64 = indptr_dtype == AKV_I64;
-  a.window = sliding_window < 0 ? -1 : sliding_window;
+  // as the extend kernel this replaces, a window applies only when it is
+  // positive (akv/system/sglang.patch:527-541): 0 means plain causal
+  a.window = sliding_window > 0 ? sliding_window : -1;
   a.scale_log2 = scale * kLog2e;
   a.out_f32 = out_dtype == AKV_F32;
   a.group = q_heads / kv_heads;

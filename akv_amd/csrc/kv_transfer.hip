@@ -11,10 +11,13 @@
 // 201-259), and a direct pool-to-pool copy -- to a peer GPU's pool when the
 // destination pointers are peer (xGMI) addresses.
 //
-// Rows of an even number of 16-byte chunks (up to 2 KiB): a workgroup per
-// token with layer rows side by side, double-buffered over the layers (the
-// Reposition's structure without the rotation).  Other sizes: flat 16-byte
-// work items, kBatch independent loads in flight per thread.
+// Rows of up to 8 KiB: one wave per row (several rows per wave when a row is
+// under 1 KiB), rows numbered layer-major -- (layer, K/V) outermost, token
+// innermost -- so the whole grid sweeps one layer's buffers at a time.  On
+// MI355X this measured ~4% faster than a workgroup per token walking its
+// layers, for the same random 1 KiB rows; with no slot vectors on either
+// side it is a streaming copy.  Longer rows: flat 16-byte work items,
+// kBatch independent loads in flight per thread.
 #include "common.h"
 
 namespace akv {
@@ -74,48 +77,66 @@ __global__ void __launch_bounds__(kThreads) copy_kv_rows_kernel(const CopyArgs a
   }
 }
 
-// Row-structured variant for rows of an even number of chunks (at most 128):
-// a workgroup per token, `rows` layer rows side by side, each lane moving
-// chunks j and j + lanes of the K and the V row; the next layer's loads are
-// in flight while this layer is stored.
-struct RowChunks {
-  u32x4 k0, k1, v0, v1;
-};
-
-__global__ void __launch_bounds__(1024) copy_kv_rows_vec_kernel(const CopyArgs a, int lanes, int rows) {
-  const int64_t t = blockIdx.x;
-  const int sub = threadIdx.x / lanes;
-  const int j = threadIdx.x - sub * lanes;
-  if (sub >= rows || t >= a.n) return;
-  const int64_t s = a.src_slots ? a.src_slots[t] : t;
-  const int64_t d = a.dst_slots ? a.dst_slots[t] : t;
-  auto load = [&](int l) {
-    const char* k = reinterpret_cast<const char*>(a.src_k[l]) + s * a.src_k_stride + 16 * j;
-    const char* v = reinterpret_cast<const char*>(a.src_v[l]) + s * a.src_v_stride + 16 * j;
-    RowChunks r;
-    r.k0 = *((const global_u32x4*)k);
-    r.k1 = *((const global_u32x4*)(k + 16 * lanes));
-    r.v0 = *((const global_u32x4*)v);
-    r.v1 = *((const global_u32x4*)(v + 16 * lanes));
-    return r;
-  };
-  auto store = [&](int l, const RowChunks& r) {
-    char* k = reinterpret_cast<char*>(a.dst_k[l]) + d * a.dst_k_stride + 16 * j;
-    char* v = reinterpret_cast<char*>(a.dst_v[l]) + d * a.dst_v_stride + 16 * j;
-    *((global_u32x4*)k) = r.k0;
-    *((global_u32x4*)(k + 16 * lanes)) = r.k1;
-    *((global_u32x4*)v) = r.v0;
-    *((global_u32x4*)(v + 16 * lanes)) = r.v1;
-  };
-  if (sub >= a.n_layers) return;
-  RowChunks cur = load(sub);
-  for (int l = sub; l < a.n_layers; l += rows) {
-    const int next = l + rows;
-    RowChunks nxt = cur;
-    if (next < a.n_layers) nxt = load(next);
-    store(l, cur);
-    cur = nxt;
+// Layer-major row copy: grid (token blocks, layers x {K, V}) -- blocks are
+// dispatched x fastest, so the grid sweeps one layer's K (then V) rows before
+// the next layer's.  2^shift lanes per row (at most 64), 64 >> shift rows per
+// wave, each lane moving chunks c, c + lanes, ... (at most U): all loads,
+// then all stores.  No division anywhere.  SRC / DST: the side has a slot
+// vector (a compile-time choice: a branch on the pointer measured 2.5%
+// slower).
+template <int U, bool SRC, bool DST>
+__global__ void __launch_bounds__(256) copy_rows_layer_major(const CopyArgs a, int shift) {
+  const int lane = threadIdx.x & 63;
+  const int lanes = 1 << shift;
+  const int c0 = lane & (lanes - 1);
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t t = (wave << (6 - shift)) + (lane >> shift);
+  if (t >= a.n) return;
+  const int l = static_cast<int>(blockIdx.y >> 1);
+  const bool kv = blockIdx.y & 1;
+  const int64_t s = SRC ? static_cast<int64_t>(a.src_slots[t]) : t;
+  const int64_t d = DST ? static_cast<int64_t>(a.dst_slots[t]) : t;
+  const char* src = reinterpret_cast<const char*>(kv ? a.src_v[l] : a.src_k[l]) + s * (kv ? a.src_v_stride : a.src_k_stride);
+  char* dst = reinterpret_cast<char*>(kv ? a.dst_v[l] : a.dst_k[l]) + d * (kv ? a.dst_v_stride : a.dst_k_stride);
+  u32x4 v[U];
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const int c = c0 + k * lanes;
+    if (c < a.chunks) v[k] = *((const global_u32x4*)(src + 16 * c));
   }
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const int c = c0 + k * lanes;
+    if (c < a.chunks) *((global_u32x4*)(dst + 16 * c)) = v[k];
+  }
+}
+
+template <int U>
+void launch_sides(int sides, dim3 grid, hipStream_t st, const CopyArgs& a, int shift) {
+  switch (sides) {
+    case 3:
+      hipLaunchKernelGGL((copy_rows_layer_major<U, true, true>), grid, dim3(256), 0, st, a, shift);
+      break;
+    case 2:
+      hipLaunchKernelGGL((copy_rows_layer_major<U, true, false>), grid, dim3(256), 0, st, a, shift);
+      break;
+    case 1:
+      hipLaunchKernelGGL((copy_rows_layer_major<U, false, true>), grid, dim3(256), 0, st, a, shift);
+      break;
+    default:
+      hipLaunchKernelGGL((copy_rows_layer_major<U, false, false>), grid, dim3(256), 0, st, a, shift);
+  }
+}
+
+void launch_layer_major(int u, int sides, dim3 grid, hipStream_t st, const CopyArgs& a, int shift) {
+  if (u == 1)
+    launch_sides<1>(sides, grid, st, a, shift);
+  else if (u == 2)
+    launch_sides<2>(sides, grid, st, a, shift);
+  else if (u == 4)
+    launch_sides<4>(sides, grid, st, a, shift);
+  else
+    launch_sides<8>(sides, grid, st, a, shift);
 }
 
 }  // namespace
@@ -150,17 +171,20 @@ extern "C" int akv_copy_kv_rows(const uint64_t* src_k_ptrs, const uint64_t* src_
   a.n = n_tokens;
   a.n_layers = n_layers;
   a.chunks = static_cast<int32_t>(row_bytes / 16);
-  if (a.chunks % 2 == 0 && a.chunks <= 128) {
-    // one workgroup per token, ~192 threads: layer rows side by side,
-    // balanced over the passes
-    const int lanes = a.chunks / 2;
-    int rows = 192 / lanes < 1 ? 1 : 192 / lanes;
-    if (rows > n_layers) rows = n_layers;
-    const int passes = (n_layers + rows - 1) / rows;
-    rows = (n_layers + passes - 1) / passes;
-    if (n_tokens > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_copy_kv_rows: too many tokens");
-    hipLaunchKernelGGL(copy_kv_rows_vec_kernel, dim3(static_cast<unsigned>(n_tokens)), dim3(lanes * rows), 0,
-                       as_stream(stream), a, lanes, rows);
+  if (a.chunks <= 512 && n_layers <= 32767) {
+    // lanes per row: the power of two covering the row, at most a wave
+    int shift = 0;
+    while ((1 << shift) < a.chunks && shift < 6) ++shift;
+    const int lanes = 1 << shift;
+    const int per_lane = (a.chunks + lanes - 1) / lanes;
+    const int64_t waves = (n_tokens + (64 >> shift) - 1) >> (6 - shift);
+    const int64_t blocks = (waves + 3) / 4;
+    if (blocks > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_copy_kv_rows: too many tokens");
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(2 * n_layers));
+    hipStream_t st = as_stream(stream);
+    const int u = per_lane == 1 ? 1 : per_lane == 2 ? 2 : per_lane <= 4 ? 4 : 8;
+    const int sides = (src_slots ? 2 : 0) + (dst_slots ? 1 : 0);
+    launch_layer_major(u, sides, grid, st, a, shift);
     return check_launch("akv_copy_kv_rows");
   }
   // any other row size: flat 16-byte work items, about 16 per thread

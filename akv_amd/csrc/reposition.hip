@@ -221,8 +221,10 @@ struct RowMover {
     r.vb = reinterpret_cast<char*>(static_cast<uintptr_t>(a.v_ptrs[layer]));
     r.k1 = load16<ALIGNED>(at(r.kb, k_src, ko1));
     r.k2 = NEOX ? load16<ALIGNED>(at(r.kb, k_src, ko2)) : make_u32x4(0, 0, 0, 0);
-    if (has_v0) r.v[0] = load16<ALIGNED>(at(r.vb, v_src, vo0));
-    if (has_v1) r.v[1] = load16<ALIGNED>(at(r.vb, v_src, vo1));
+    // without a K tail a NeoX lane moves exactly two V units and a GPT-J lane
+    // one (the V row has 2 or 1 units per lane): no per-lane predicate
+    if (WIDE ? has_v0 : true) r.v[0] = load16<ALIGNED>(at(r.vb, v_src, vo0));
+    if (WIDE ? has_v1 : NEOX) r.v[1] = load16<ALIGNED>(at(r.vb, v_src, vo1));
     return r;
   }
 
@@ -230,8 +232,8 @@ struct RowMover {
   __device__ __forceinline__ void finish(const RowData& r) const {
     // V first: it needs no arithmetic, and its registers free up before the
     // rotation's
-    if (has_v0) store16<ALIGNED>(at(r.vb, v_dst, vo0), r.v[0]);
-    if (has_v1) store16<ALIGNED>(at(r.vb, v_dst, vo1), r.v[1]);
+    if (WIDE ? has_v0 : true) store16<ALIGNED>(at(r.vb, v_dst, vo0), r.v[0]);
+    if (WIDE ? has_v1 : NEOX) store16<ALIGNED>(at(r.vb, v_dst, vo1), r.v[1]);
     u32x4 o1 = r.k1, o2 = r.k2;
     if (!same) {
       // two pairs at a time: their ten coefficients are read from LDS just
@@ -351,11 +353,18 @@ __global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionAr
     }
   }
   // one 16-byte-unaligned layer base sends the whole workgroup down the
-  // element-wise path (a uniform branch); the flag rides on the barrier
-  bool misaligned = false;
-  for (int l = threadIdx.x; l < a.n_layers; l += blockDim.x)
-    misaligned |= ((a.k_ptrs[l] | a.v_ptrs[l]) & 15) != 0;
-  const bool aligned = !__syncthreads_or(misaligned);
+  // element-wise path (a uniform branch): the first wave takes the vote and
+  // publishes it in LDS before the one barrier
+  __shared__ int any_misaligned;
+  const int first_wave = blockDim.x < 64 ? static_cast<int>(blockDim.x) : 64;
+  if (static_cast<int>(threadIdx.x) < first_wave) {
+    bool bad = false;
+    for (int l = threadIdx.x; l < a.n_layers; l += first_wave) bad |= ((a.k_ptrs[l] | a.v_ptrs[l]) & 15) != 0;
+    const bool any = __ballot(bad) != 0;
+    if (threadIdx.x == 0) any_misaligned = any;
+  }
+  __syncthreads();
+  const bool aligned = !any_misaligned;
   if (!live || row_sub >= a.n_layers) return;
 
   constexpr int64_t B = sizeof(T);

@@ -248,7 +248,7 @@ class PagedInputs:
         return max(self.n_tokens) if self.n_tokens else 0
 
 
-def _paged_counts(keep, final, page_size):
+def _paged_counts(keep, birth, final, page_size):
     n = len(keep)
     kept = int(keep.sum())
     if not np.array_equal(final[keep], np.arange(kept)):
@@ -256,6 +256,11 @@ def _paged_counts(keep, final, page_size):
     dropped = np.flatnonzero(~keep)
     p0 = int(dropped[0]) // page_size if len(dropped) else -(-n // page_size)
     copy_from = p0 * page_size
+    # pages below p0 stay in place, unrotated: their tokens must already sit
+    # at their final positions
+    if not np.array_equal(birth[:copy_from], np.arange(copy_from)):
+        raise ValueError("paged compaction keeps the pages before the first drop in place: their tokens' "
+                         "birth positions must equal their ranks")
     copies = max(0, kept - copy_from)
     new_pages = -(-kept // page_size)
     fresh = max(0, new_pages - p0)
@@ -276,10 +281,11 @@ def pack_paged_inputs(layouts, page_size, device):
     for layout in layouts:
         keep = np.asarray(layout.keep_mask, dtype=bool)
         final = np.asarray(layout.positions, dtype=np.int32)
+        birth = np.asarray(layout.birth_positions, dtype=np.int32)
         keeps.append(keep)
-        births.append(np.asarray(layout.birth_positions, dtype=np.int32))
+        births.append(birth)
         finals.append(final)
-        stats.append((len(keep),) + _paged_counts(keep, final, page_size))
+        stats.append((len(keep),) + _paged_counts(keep, birth, final, page_size))
     B = len(stats)
     ns = [s[0] for s in stats]
     bases = np.zeros((6, B + 1), dtype=np.int64)

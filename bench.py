@@ -26,6 +26,7 @@ batch.
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -50,7 +51,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="gpt-oss-32k")
     p.add_argument("--latency-iters", type=int, default=100)
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--cpu-runs", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-cow", action="store_true", help="skip the page-16 copy-on-write configuration")
     p.add_argument("--reposition-only", action="store_true",
@@ -693,6 +694,67 @@ def prefill_llama_config(device, flush, extend=4096):
     return {"workload": f"llama3-8b prefill of {extend} tokens over {plen} kept tokens (32 q / 8 KV heads x 128)", **r}
 
 
+def ceiling_legs(pipe, steps, warmup, flush):
+    """Ceilings of the Reposition's access pattern, timed in the same run.
+
+    * gather copy: ``akv_copy_kv_rows`` of the same source -> destination K
+      and V rows of every layer (no arithmetic, one launch), in the order the
+      copy lists hold (raw token order), sorted by source slot and sorted by
+      destination slot;
+    * streaming copy: the same kernel between two packed buffers of the same
+      byte count (no slot lists: consecutive rows);
+    * the Reposition itself with its lists permuted into the same two sorted
+      orders (its output does not depend on the order: destinations are
+      disjoint).
+    Rates: K/V bytes read + written per launch / average launch time; the
+    Reposition's rate counts its algorithmic bytes (slot lists and table rows
+    as well), as ``roofline.achieved`` does."""
+    from akv_amd import transfer
+
+    o, p, m = pipe.out, pipe.pool, pipe.w.model
+    n = pipe.moved
+    kv_bytes = pipe.retained_bytes
+
+    def rate(ms, nbytes):
+        return round(nbytes / (ms / 1e3) / 1e9, 1)
+
+    orders = {"raw": None, "by_source_slot": torch.argsort(o.copy_src), "by_destination_slot": torch.argsort(o.copy_dst)}
+    out = {"gather_copy_GBs": {}, "reposition_GBs": {}}
+    for name, perm in orders.items():
+        src = o.copy_src if perm is None else o.copy_src[perm].contiguous()
+        dst = o.copy_dst if perm is None else o.copy_dst[perm].contiguous()
+        pairs = o.copy_pairs if perm is None else o.copy_pairs[perm].contiguous()
+
+        def gather():
+            transfer.copy_kv_rows(p.k_ptrs, p.v_ptrs, p.k[0], p.k_ptrs, p.v_ptrs, p.k[0], n, src_slots=src,
+                                  dst_slots=dst)
+
+        def repo():
+            ops.reposition_kv_layers(p.k_ptrs, p.v_ptrs, p.k[0], p.v[0], src, dst, pairs, pipe.rope,
+                                     is_neox_style=m.is_neox_style)
+
+        warm, _ = _time_steps(gather, steps, warmup, 0, flush)
+        out["gather_copy_GBs"][name] = rate(warm, kv_bytes)
+        warm, _ = _time_steps(repo, steps, warmup, 0, flush)
+        out["reposition_GBs"][name] = rate(warm, pipe.alg_bytes)
+    a = transfer.PackedKV.empty(m.n_layers, n, m.n_heads, m.head_dim, m.dtype, pipe.device)
+    b = transfer.PackedKV.empty(m.n_layers, n, m.n_heads, m.head_dim, m.dtype, pipe.device)
+    a.k.fill_(1.0)
+    a.v.fill_(1.0)
+
+    def stream():
+        transfer.copy_kv_rows(a.k_ptrs, a.v_ptrs, a.k[0], b.k_ptrs, b.v_ptrs, b.k[0], n)
+
+    warm, _ = _time_steps(stream, steps, warmup, 0, flush)
+    out["streaming_copy_GBs"] = rate(warm, kv_bytes)
+    del a, b
+    torch.cuda.empty_cache()
+    out["reposition_frac_of_gather"] = round(out["reposition_GBs"]["raw"] / out["gather_copy_GBs"]["raw"], 4)
+    out["reposition_frac_of_streaming"] = round(out["reposition_GBs"]["raw"] / out["streaming_copy_GBs"], 4)
+    out["kernel"] = "akv_copy_kv_rows (layer-major, one 1 KiB row per wave)"
+    return out
+
+
 def read_pmc_traffic():
     """HBM bytes per Reposition launch from the committed rocprof PMC summary."""
     if not PMC_SUMMARY.exists():
@@ -703,64 +765,84 @@ def read_pmc_traffic():
     return None
 
 
-def cpu_baseline(pipe, seconds):
-    """The CPU oracle (numpy port of the reference path) on a bounded sample."""
+def cpu_threads():
+    """Host threads the baseline may use: OMP_NUM_THREADS when set (the GPU
+    box sets it to its CPU share), else the CPUs this process may run on."""
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(pipe, runs):
+    """The reference path restated on the host CPU, same workload, same run.
+
+    Per run: the Drop + Reposition event compile (``oracle.events``, Python,
+    single thread, as the reference's host compiler), the table update /
+    freed list / copy lists (``oracle.occurrence``, numpy), the Reposition of
+    all moved tokens over all layers (``oracle.cpu_torch``, torch CPU fp32
+    vectorised over every host thread) and the decode indices.  Reported:
+    p50 over ``runs`` runs; ``value`` = retained-KV bytes / p50 of the
+    Reposition alone (the metric's unit), and the whole step's p50 beside it.
+    The CPU result of the last run is compared bit for bit with the GPU's
+    over every destination row of every layer."""
+    from oracle import cpu_torch
     from oracle import events as oe
     from oracle import occurrence as occ
-    from oracle import reposition as rp
 
-    w, lay = pipe.w, pipe.layouts[0]
-    m = w.model
-    ev = synth.request_events(pipe.n, w.spans[0])
-    t0 = time.perf_counter()
-    ref = oe.compile_context_layout(*(ev[k].numpy() for k in ev))
-    compile_s = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    cf = occ.closed_form(pipe.slots.birth_rows[0], ref.keep_mask, ref.birth_positions, ref.positions,
-                         pipe.slots.fresh[0])
-    tables_s = time.perf_counter() - t0
-    # Reposition on a sample of moved tokens across all layers: gather the
-    # sample's source rows into a compact host pool and move them with the oracle
-    rng = np.random.default_rng(0)
-    table = pipe.rope.cpu().numpy()
-    src_all = cf["copy_source_slots"]
-    pairs_all = cf["copy_position_pairs"]
-
-    def run(count):
-        idx = np.sort(rng.choice(len(src_all), size=count, replace=False))
-        s = torch.from_numpy(src_all[idx].astype(np.int64)).to(pipe.device)
-        k = [t[s].cpu().view(torch.int16).numpy().view(np.uint16) for t in pipe.pool.k]
-        v = [t[s].cpu().view(torch.int16).numpy().view(np.uint16) for t in pipe.pool.v]
-        k = [np.concatenate((x, np.zeros_like(x))) for x in k]
-        v = [np.concatenate((x, np.zeros_like(x))) for x in v]
-        t = time.perf_counter()
-        rp.reposition_kv_layers(k, v, np.arange(count), np.arange(count, 2 * count), pairs_all[idx], table,
-                                dtype="bf16")
-        return time.perf_counter() - t
-
-    probe = min(256, len(src_all))
-    dt = run(probe)
-    per_token = dt / probe
-    count = int(min(len(src_all), max(probe, seconds / max(per_token, 1e-9))))
-    dt = run(count)
-    per_token = dt / count
-    full_s = compile_s + tables_s + per_token * len(src_all)
-    bytes_per_token = 4 * m.n_layers * m.n_heads * m.head_dim * 2
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    w, m = pipe.w, pipe.w.model
+    ev = {k: v.numpy() for k, v in synth.request_events(pipe.n, w.spans[0]).items()}
+    # the GPU result at every destination row, then host copies of the pool
+    pipe.reposition()
+    torch.cuda.synchronize()
+    dst = pipe.out.copy_dst.long()
+    gpu_k = [t[dst].cpu() for t in pipe.pool.k]
+    gpu_v = [t[dst].cpu() for t in pipe.pool.v]
+    host_k = [t.cpu() for t in pipe.pool.k]
+    host_v = [t.cpu() for t in pipe.pool.v]
+    table = pipe.rope.cpu()
+    step_s, repo_s = [], []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        lay = oe.compile_context_layout(*(ev[k] for k in ("token_ids", "drop_insert_offsets", "drop_range_offsets",
+                                                          "drop_ranges", "reposition_raw_boundaries",
+                                                          "reposition_insert_offsets")))
+        cf = occ.closed_form(pipe.slots.birth_rows[0], lay.keep_mask, lay.birth_positions, lay.positions,
+                             pipe.slots.fresh[0])
+        t1 = time.perf_counter()
+        cpu_torch.reposition_kv_layers(host_k, host_v, cf["copy_source_slots"], cf["copy_destination_slots"],
+                                       cf["copy_position_pairs"], table, is_neox_style=m.is_neox_style)
+        t2 = time.perf_counter()
+        np.concatenate((cf["active_slots"], [int(pipe.slots.fresh[0][0])]))  # decode indices, one new token
+        t3 = time.perf_counter()
+        step_s.append(t3 - t0)
+        repo_s.append(t2 - t1)
+    cdst = torch.from_numpy(cf["copy_destination_slots"].astype(np.int64))
+    exact = bool(torch.equal(cdst, dst.cpu())) and all(
+        torch.equal(h[cdst].view(torch.int16), g.view(torch.int16)) for h, g in zip(host_k + host_v, gpu_k + gpu_v))
+    del host_k, host_v, gpu_k, gpu_v
+    repo_p50 = percentile(repo_s, 50)
+    step_p50 = percentile(step_s, 50)
     chunked_s = _chunked_ownership_port()
     return {
-        "value": round(bytes_per_token * count / dt / 1e9, 4),
+        "value": round(pipe.retained_bytes / repo_p50 / 1e9, 3),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": (f"numpy oracle, single thread: Reposition of {count} of {len(src_all)} moved tokens x "
-                   f"{m.n_layers} layers ({dt:.2f} s); event compile {compile_s * 1e3:.1f} ms and table "
-                   f"closed form {tables_s * 1e3:.1f} ms on the full request; full-request estimate "
-                   f"{full_s * 1e3:.0f} ms"),
-        "full_request_ms_estimate": round(full_s * 1e3, 1),
+        "sample": (f"the whole 32k GPT-OSS request, {runs} runs: Reposition of all {pipe.moved} moved tokens x "
+                   f"{m.n_layers} layers in torch CPU fp32 on {threads} threads (oracle.cpu_torch), plus the "
+                   f"Python event compile and numpy tables of the same step"),
+        "reposition_p50_ms": round(repo_p50 * 1e3, 1),
+        "step_p50_ms": round(step_p50 * 1e3, 1),
+        "step_value_GBs": round(pipe.retained_bytes / step_p50 / 1e9, 3),
+        "runs": runs,
+        "bit_exact_vs_gpu": exact,
         "chunked_ownership_ms": round(chunked_s * 1e3, 1),
         "chunked_ownership_sample": (f"numpy oracle of the chunked-prefill ownership (window, plan, advance, "
                                      f"publication; {CHUNKS} chunks of the 32768-token trajectory), host time"),
-        "host": host_info(),
+        "host": host_info(threads),
     }
 
 
@@ -792,16 +874,21 @@ def _chunked_ownership_port():
     return time.perf_counter() - t0
 
 
-def host_info():
-    model = ""
+def host_info(threads):
+    """lscpu model name and core counts of this host."""
+    info = {}
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return {"cpu": model, "logical_cpus": os.cpu_count(), "torch_threads": torch.get_num_threads()}
+    cores_per_socket = int(info.get("Core(s) per socket", "0") or 0)
+    sockets = int(info.get("Socket(s)", "0") or 0)
+    return {"cpu": info.get("Model name", ""), "physical_cores": cores_per_socket * sockets or None,
+            "logical_cpus": os.cpu_count(), "cpus_available": len(os.sched_getaffinity(0)),
+            "torch_threads": threads}
 
 
 def percentile(xs, q):
@@ -884,7 +971,7 @@ def main():
     # the same launch with every pair at its birth position: a pure row copy
     # of the same slots (same bytes, no rotation) -- the access pattern's own
     # rate, against which the rotation's cost shows
-    copy_only = None
+    copy_only = ceiling = None
     if not args.reposition_only:
         o, p, neox = pipe.out, pipe.pool, pipe.w.model.is_neox_style
         same = torch.stack((o.copy_pairs[:, 0], o.copy_pairs[:, 0]), 1).contiguous()
@@ -896,6 +983,8 @@ def main():
         warm_copy, _ = _time_steps(copy_step, args.steps, args.warmup, 0, pipe.flush)
         copy_only = {"ms": round(warm_copy, 5),
                      "pct_hbm_peak": round(100 * pipe.alg_bytes / (warm_copy / 1e3) / 1e9 / HBM_PEAK_GBS, 2)}
+        print("# ceiling legs ...", file=sys.stderr, flush=True)
+        ceiling = ceiling_legs(pipe, args.steps, args.warmup, pipe.flush)
 
     # roofline of the dominant kernel: its average launch inside the timed
     # (back-to-back, steady-state) region
@@ -937,6 +1026,8 @@ def main():
         "reposition_steady_ms": round(float(np.mean(repo_timed_ms)), 5),
         # same slots, pairs at the birth position (a bit copy, no rotation)
         "reposition_copy_only": copy_only,
+        # the access pattern's own ceilings, same run (see ceiling_legs)
+        "ceiling": ceiling,
         "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         # compaction: count + scatter (one request spans 128 tiles, under the
         # fused-offsets limit) ; Reposition: one launch for the 36-layer group
@@ -965,7 +1056,7 @@ def main():
             result["other_configs"].append(cow_config(device, pipe.flush))
     if not args.no_cpu_baseline:
         print("# cpu baseline ...", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(pipe, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(pipe, args.cpu_runs)
     print(json.dumps(result), flush=True)
 
 

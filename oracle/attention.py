@@ -55,8 +55,10 @@ def context_attention(q, k_ext, v_ext, k_pool, v_pool, qo_indptr, kv_indptr, kv_
     ``qo_indptr[s]..qo_indptr[s+1]`` and prefix keys
     ``kv_indices[kv_indptr[s]..kv_indptr[s+1]]`` (pool rows, all visible),
     then its own keys ``k_ext``/``v_ext`` causally (key ``j <= i``).  With
-    ``window >= 0`` a key is visible only when ``q_pos <= k_pos + window``;
-    without positions ``q_pos = prefix_length + i`` and prefix ``k_pos = j``.
+    ``window > 0`` a key is visible only when ``q_pos <= k_pos + window``
+    (the extend kernel applies no window for 0 or less,
+    ``akv/system/sglang.patch:527-541``); without positions
+    ``q_pos = prefix_length + i`` and prefix ``k_pos = j``.
 
     ``q``: [Nq, Hq, D]; ``k_ext``/``v_ext``: [Nq, Hkv, D]; ``k_pool``/``v_pool``:
     [slots, Hkv, D].  Returns [Nq, Hq, D] float32.
@@ -90,7 +92,7 @@ def context_attention(q, k_ext, v_ext, k_pool, v_pool, qo_indptr, kv_indptr, kv_
             vis = np.zeros(plen + b - a, dtype=bool)
             vis[:plen] = True
             vis[plen : plen + i + 1] = True
-            if window >= 0:
+            if window > 0:
                 vis &= qpos[i] <= keys_pos + window
             for h in range(hq):
                 g = h // group

@@ -57,6 +57,9 @@ def compact_pages(row, keep, birth_positions, final_positions, fresh_pages, page
     if not np.array_equal(final[kept_idx], np.arange(len(kept_idx))):
         raise ValueError("paged compaction needs compact final positions (0 .. kept - 1)")
     p0 = first_copied_page(keep, P)
+    # the pages before the first drop stay in place, unrotated
+    if not np.array_equal(birth[: p0 * P], np.arange(min(n, p0 * P))):
+        raise ValueError("pages kept in place need birth positions equal to their ranks")
     fresh_pages = np.asarray(fresh_pages, dtype=np.int64)
     need = max(0, -(-len(kept_idx) // P) - p0)
     if len(fresh_pages) != need:

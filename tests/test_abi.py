@@ -61,6 +61,13 @@ def test_validation_rejects_before_any_device_work(lib):
     assert "null device pointer" in _lib.last_error()
     assert lib.akv_bind_workspace_bytes(4, 100000) > 0
     assert lib.akv_context_attention(*zeros(lib.akv_context_attention, a15=1, a17=1, a18=64, a34=4)) == _lib.AKV_EINVAL
+    # prefix indices without K/V pools: rejected instead of faulting on the
+    # null pool (addresses are never dereferenced on this path)
+    fake = 1 << 20
+    args = zeros(lib.akv_context_attention, a0=fake, a3=fake, a4=fake, a15=1, a16=8, a17=1, a18=64, a19=fake,
+                 a20=fake, a22=fake, a29=0.125, a30=fake, a34=4)
+    assert lib.akv_context_attention(*args) == _lib.AKV_EINVAL
+    assert "without K/V pools" in _lib.last_error()
     assert lib.akv_window_count(*zeros(lib.akv_window_count)) == _lib.AKV_EINVAL
     assert lib.akv_window_compile_bounded(*zeros(lib.akv_window_compile_bounded)) == _lib.AKV_EINVAL
     assert "null host pointer" in _lib.last_error()

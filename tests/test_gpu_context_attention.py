@@ -69,7 +69,8 @@ P_LENS = [0, 5, 64, 1000, 0, 37, 130]
 
 
 @pytest.mark.parametrize("d,hq,hkv", [(64, 64, 8), (128, 32, 8)])
-@pytest.mark.parametrize("window,positions", [(-1, False), (24, True), (24, False)])
+# window 0 is no window, as in the extend kernel the prefill replaces
+@pytest.mark.parametrize("window,positions", [(-1, False), (24, True), (24, False), (0, True)])
 @pytest.mark.parametrize("with_sinks", [True, False])
 def test_segments_match_oracle(device, d, hq, hkv, window, positions, with_sinks):
     c = _case(device, hq, hkv, d, Q_LENS, P_LENS, seed=d + hq + window + with_sinks)

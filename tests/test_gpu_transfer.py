@@ -75,11 +75,13 @@ def test_validation(device):
                                                                                     device=device))
 
 
-@pytest.mark.parametrize("layers,heads,dim", [(37, 8, 64), (5, 1, 8), (4, 3, 40), (3, 16, 128), (2, 1, 1024)])
+@pytest.mark.parametrize("layers,heads,dim", [(37, 8, 64), (5, 1, 8), (4, 3, 40), (3, 1, 264), (3, 16, 128),
+                                               (2, 1, 1024), (2, 8, 1024)])
 def test_row_sizes_and_layer_counts(device, layers, heads, dim):
-    """Rows of 1, 15, 64, 128 and 256 16-byte chunks: the per-token kernel
-    (even chunk counts up to 128, layer rows side by side over uneven passes)
-    and the flat kernel (any other size) copy the same rows."""
+    """Rows of 64, 1, 15, 33, 256, 128 and 1024 16-byte chunks: the
+    layer-major kernel with several rows per wave (1 and 15 chunks), one row
+    per wave with one to eight chunks per lane (33 to 512 chunks), and the
+    flat kernel (longer rows) copy the same rows."""
     slots = 3000
     ks, vs, kp, vp = _pool(device, layers, slots, heads, dim, seed=layers + dim)
     ks2, vs2, kp2, vp2 = _pool(device, layers, slots, heads, dim, seed=layers + dim + 1)

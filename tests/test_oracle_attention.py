@@ -1,6 +1,7 @@
 """Pins oracle.attention against torch SDPA and the reference's sink formula."""
 
 import numpy as np
+import pytest
 import torch
 
 from oracle import attention as at
@@ -121,6 +122,24 @@ def test_context_window_matches_searchsorted_gather():
             mask = np.ones((1, end - start), dtype=bool)
             want = _sdpa(q[a + i : a + i + 1], keys_k[start:end], keys_v[start:end], mask, 0.5)
             np.testing.assert_allclose(got[a + i], want[0], atol=1e-6, rtol=1e-5)
+
+
+@pytest.mark.parametrize("window", [0, -1, -5])
+def test_context_window_zero_or_negative_is_causal(window):
+    # the extend kernel applies a window only when it is positive
+    # (sglang.patch:527-541): 0 and negative values are plain causal
+    # attention over the prefix, not "keys at the query's own position only"
+    rng = np.random.default_rng(8)
+    q, ke, ve, kp, vp, qo, kv, idx = _segments(rng, 4, 2, 8, [7, 3], [5, 0])
+    kpos = np.arange(5)
+    qpos = np.r_[np.arange(5, 12), np.arange(3)]
+    base = at.context_attention(q, ke, ve, kp, vp, qo, kv, idx, 0.5, q_positions=qpos, kv_positions=kpos)
+    got = at.context_attention(q, ke, ve, kp, vp, qo, kv, idx, 0.5, window=window, q_positions=qpos,
+                               kv_positions=kpos)
+    np.testing.assert_array_equal(got, base)
+    # and a window of 1 does restrict (each query sees keys at q_pos - 1 .. q_pos)
+    one = at.context_attention(q, ke, ve, kp, vp, qo, kv, idx, 0.5, window=1, q_positions=qpos, kv_positions=kpos)
+    assert not np.allclose(one, base)
 
 
 def test_context_sinks_scale_by_sigmoid_of_lse():

@@ -84,3 +84,23 @@ def test_page_sixteen_conservation_and_placement():
         first = pg.first_drop(lay.keep_mask)
         same = pairs[:, 0] == pairs[:, 1]
         np.testing.assert_array_equal(same, pairs[:, 1] < first)
+
+
+def test_pages_kept_in_place_need_birth_at_rank():
+    import pytest
+
+    n, P = 64, 16
+    keep = np.ones(n, dtype=bool)
+    keep[40:44] = False
+    final = np.where(keep, np.cumsum(keep) - 1, -1)
+    row = np.arange(1, n + 1) * 1
+    birth = np.arange(n)
+    fresh = np.array([100])  # kept 60 -> 4 pages, p0 = 2 -> 2 fresh pages
+    with pytest.raises(ValueError, match="need 2 fresh pages"):
+        pg.compact_pages(row, keep, birth, final, fresh, P)
+    out = pg.compact_pages(row, keep, birth, final, np.array([100, 101]), P)
+    assert out["first_copied_page"] == 2
+    bad = birth.copy()
+    bad[3] = 9
+    with pytest.raises(ValueError, match="birth positions equal to their ranks"):
+        pg.compact_pages(row, keep, bad, final, np.array([100, 101]), P)

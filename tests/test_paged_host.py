@@ -99,3 +99,28 @@ def test_pack_paged_inputs_rejects_uncompacted_positions():
     )
     with pytest.raises(ValueError, match="compact final positions"):
         tables.pack_paged_inputs([lay], 16, "cpu")
+
+
+def test_pack_paged_inputs_rejects_prefix_births_off_rank():
+    """Pages before the first drop stay in place, unrotated, so their tokens
+    must already sit at their final positions.  Compiled event programs
+    always satisfy this (no drop precedes those tokens); a hand-made layout
+    that does not is rejected instead of leaving stale rotations behind."""
+    from types import SimpleNamespace
+
+    n, P = 64, 16
+    keep = np.ones(n, dtype=bool)
+    keep[40:44] = False
+    final = np.where(keep, np.cumsum(keep) - 1, -1).astype(np.int32)
+    birth = np.arange(n, dtype=np.int32)
+    ok = SimpleNamespace(keep_mask=keep, positions=final, birth_positions=birth)
+    tables.pack_paged_inputs([ok], P, "cpu")
+    bad_birth = birth.copy()
+    bad_birth[5] = 7
+    bad = SimpleNamespace(keep_mask=keep, positions=final, birth_positions=bad_birth)
+    with pytest.raises(ValueError, match="birth positions must equal their ranks"):
+        tables.pack_paged_inputs([bad], P, "cpu")
+    # the same token past the first copied page is a copy with pair (birth, rank): accepted
+    late = birth.copy()
+    late[50] = 52
+    tables.pack_paged_inputs([SimpleNamespace(keep_mask=keep, positions=final, birth_positions=late)], P, "cpu")
