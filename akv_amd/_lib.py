@@ -63,6 +63,12 @@ _SIGNATURES = {
          c_int32, c_int32, _P, _P, _P, ctypes.c_float, _P, c_int32, c_int64, c_int64, c_int64,
          _P, c_int64, _P],
     ),
+    "akv_decode_attention_noalloc_max_bytes": (c_int64, []),
+    "akv_decode_attention_noalloc": (
+        c_int32,
+        [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int32, c_int32,
+         c_int32, c_int32, _P, _P, _P, ctypes.c_float, _P, c_int32, c_int64, c_int64, c_int64, _P],
+    ),
     "akv_context_attention": (
         c_int32,
         [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64,

@@ -20,6 +20,8 @@
 // A[l%16][4(l/16)+i] and B[4(l/16)+i][l%16] and holds D[4(l/16)+i][l%16].
 #include <cmath>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace akv {
@@ -280,6 +282,39 @@ __global__ void __launch_bounds__(kWays * D) decode_attention_combine_kernel(con
 
 int64_t chunks_for(int64_t max_len) { return max_len <= 0 ? 1 : (max_len + kChunk - 1) / kChunk; }
 
+// Split-K scratch of akv_decode_attention_noalloc: a file-scope device array,
+// one per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the
+// symbol): it uses the per-device address hipGetSymbolAddress returns.
+constexpr int64_t kScratchBytes = 32ll << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up once per device with that
+// device current.
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess)
+    return fail(AKV_EHIP, "akv_decode_attention_noalloc: hipGetDevice failed: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(AKV_EINVAL, "akv_decode_attention_noalloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p)
+      return fail(AKV_EHIP, "akv_decode_attention_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                  hipGetErrorString(err));
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return AKV_OK;
+}
+
 }  // namespace
 }  // namespace akv
 
@@ -361,4 +396,37 @@ extern "C" int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q
                        st, a);
   }
   return check_launch("akv_decode_attention (combine)");
+}
+
+extern "C" int64_t akv_decode_attention_noalloc_max_bytes(void) { return akv::kScratchBytes; }
+
+extern "C" int akv_decode_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                            const void* k_buffer, const void* v_buffer, int64_t k_stride_slot,
+                                            int64_t k_stride_head, int64_t v_stride_slot, int64_t v_stride_head,
+                                            int32_t n_requests, int32_t q_heads, int32_t kv_heads,
+                                            int32_t head_dim, const int32_t* kv_indptr, const int32_t* kv_indices,
+                                            const float* sinks, float scale, void* out, int32_t out_dtype,
+                                            int64_t out_stride_b, int64_t out_stride_h, int64_t max_len,
+                                            void* stream) {
+  using namespace akv;
+  const int64_t need = akv_decode_attention_workspace_bytes(n_requests, kv_heads > 0 ? kv_heads : 1,
+                                                            head_dim > 0 ? head_dim : 1, max_len);
+  if (need > kScratchBytes)
+    return fail(AKV_EINVAL,
+                "akv_decode_attention_noalloc: the split-K partials need %lld bytes, the static scratch holds "
+                "%lld (%d requests x %d KV heads x max_len %lld)",
+                static_cast<long long>(need), static_cast<long long>(kScratchBytes), n_requests, kv_heads,
+                static_cast<long long>(max_len));
+  if (n_requests <= 0) return akv_decode_attention(q, q_stride_b, q_stride_h, k_buffer, v_buffer, k_stride_slot,
+                                                   k_stride_head, v_stride_slot, v_stride_head, n_requests,
+                                                   q_heads, kv_heads, head_dim, kv_indptr, kv_indices, sinks,
+                                                   scale, out, out_dtype, out_stride_b, out_stride_h, max_len,
+                                                   nullptr, 0, stream);
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return akv_decode_attention(q, q_stride_b, q_stride_h, k_buffer, v_buffer, k_stride_slot, k_stride_head,
+                              v_stride_slot, v_stride_head, n_requests, q_heads, kv_heads, head_dim, kv_indptr,
+                              kv_indices, sinks, scale, out, out_dtype, out_stride_b, out_stride_h, max_len, ws,
+                              kScratchBytes, stream);
 }

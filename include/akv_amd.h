@@ -241,6 +241,30 @@ int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                          int64_t workspace_bytes, void* stream);
 
 /*
+ * akv_decode_attention without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  The split-K
+ * partials live in a static device array of
+ * akv_decode_attention_noalloc_max_bytes() bytes per GPU (32 MiB), held
+ * until the process ends; a call whose partials need more
+ * (akv_decode_attention_workspace_bytes) fails with AKV_EINVAL.  Allocates
+ * nothing.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, two host threads) race.
+ */
+int64_t akv_decode_attention_noalloc_max_bytes(void);
+int akv_decode_attention_noalloc(const void* q, int64_t q_stride_b,
+                                 int64_t q_stride_h, const void* k_buffer,
+                                 const void* v_buffer, int64_t k_stride_slot,
+                                 int64_t k_stride_head, int64_t v_stride_slot,
+                                 int64_t v_stride_head, int32_t n_requests,
+                                 int32_t q_heads, int32_t kv_heads,
+                                 int32_t head_dim, const int32_t* kv_indptr,
+                                 const int32_t* kv_indices, const float* sinks,
+                                 float scale, void* out, int32_t out_dtype,
+                                 int64_t out_stride_b, int64_t out_stride_h,
+                                 int64_t max_len, void* stream);
+
+/*
  * Prefill context attention over occurrence metadata (MFMA, bf16 in, fp32
  * accumulate).  Segment s: queries q[qo_indptr[s] .. qo_indptr[s+1]) with
  * their own keys k_ext/v_ext (causal by index) after the prefix keys
