@@ -123,7 +123,7 @@ def allocate_outputs(inputs, device, *, generated_total=None):
     """Outputs of exactly the sizes the CPU layouts fix (no device read-back)."""
     lib = _lib.load()
     i32 = torch.int32
-    ws_bytes = lib.akv_compact_workspace_bytes(inputs.n_requests, inputs.max_tokens)
+    ws_bytes = lib.akv_compact_workspace_bytes(inputs.n_requests, sum(inputs.n_tokens))
     kv = None
     indptr = None
     if generated_total is not None:
@@ -182,7 +182,7 @@ def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_po
         rc = lib.akv_compact_rows(
             inputs.n_requests,
             inputs.req_offsets.data_ptr(),
-            inputs.max_tokens,
+            sum(inputs.n_tokens),
             req_to_token.data_ptr(),
             req_to_token.stride(0),
             _lib.ptr(row_pointers),

@@ -58,7 +58,7 @@ def parse_args():
                    help="time only the Reposition launch (for profiling runs)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy 1 GiB -> 1 GiB three times (scales rocprof byte counters)")
-    p.add_argument("--only", choices=["handoff", "prefill", "prefill-llama", "chunked", "decode"],
+    p.add_argument("--only", choices=["handoff", "prefill", "prefill-llama", "chunked", "decode", "ragged"],
                    help="run one secondary configuration alone and print its line (for profiling runs)")
     return p.parse_args()
 
@@ -250,13 +250,12 @@ def ragged_config(device, flush):
     # bytes: keep + positions + birth slot read, row write, lists written
     meta = total * (1 + 8 + 4 + 4) + 4 * inputs.retired_total + 16 * inputs.moved_total \
         + 8 * inputs.kept_total + 4 * (inputs.kept_total + w.n_requests) + 12 * w.n_requests
-    entries = w.n_requests * -(-max(w.lengths) // (256 * 16))
     return {
         "workload": w.name, "requests": w.n_requests, "tokens": total, "kept": inputs.kept_total,
         "moved": inputs.moved_total, "step_ms_back_to_back": round(warm, 5),
         "step_ms_graph_replay": round(graph, 5),
         "step_p50_ms": round(percentile(cold, 50), 5), "step_p99_ms": round(percentile(cold, 99), 5),
-        "kernel_launches_per_step": 2 if entries <= 4096 else 3,
+        "kernel_launches_per_step": 2,
         "metadata_bytes": meta, "host_event_compile_ms": round(compile_ms, 1),
     }
 
@@ -913,7 +912,7 @@ def main():
         sink = torch.empty((), device=device)
         flush = lambda: torch.sum(scratch, 0, out=sink)  # noqa: E731
         run = {"handoff": handoff_config, "prefill": prefill_config, "prefill-llama": prefill_llama_config,
-               "chunked": chunked_config, "decode": decode_consumer_config}[args.only]
+               "chunked": chunked_config, "decode": decode_consumer_config, "ragged": ragged_config}[args.only]
         print(json.dumps(run(device, flush)), flush=True)
         return
     pipe = Pipeline(args.workload, device)
@@ -1029,8 +1028,8 @@ def main():
         # the access pattern's own ceilings, same run (see ceiling_legs)
         "ceiling": ceiling,
         "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
-        # compaction: count + scatter (one request spans 128 tiles, under the
-        # fused-offsets limit) ; Reposition: one launch for the 36-layer group
+        # compaction: count + scatter; Reposition: one launch for the
+        # 36-layer group
         "kernel_launches_per_step": 1 if args.reposition_only else 3,
         "roofline": {
             "bound": "hbm",

@@ -70,15 +70,18 @@ int akv_reposition_kv_layers(const uint64_t* k_ptrs, const uint64_t* v_ptrs,
                              int32_t skip_unmapped, void* stream);
 
 /*
- * Device bytes of the scratch buffer akv_compact_rows needs for a batch of
- * n_requests whose longest request has max_tokens raw tokens.
+ * Device bytes of the workspace akv_compact_rows needs for a batch of
+ * n_requests holding total_tokens raw tokens in all (16-byte aligned, no
+ * clearing needed).  Calls that share a workspace must not overlap (issue
+ * them on one stream).
  */
-int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t max_tokens);
+int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t total_tokens);
 
 /*
  * Batched page-table compaction of a single-owner final forward.  For
  * request b, raw tokens [req_offsets[b], req_offsets[b+1]) of the flat
- * keep / birth_positions / final_positions vectors; its raw row is
+ * keep / birth_positions / final_positions vectors (req_offsets[B] ==
+ * total_tokens); its raw row is
  * row_pointers[req_rows[b]] when row_pointers != NULL, else
  * table + req_rows[b] * row_stride.  The birth slots are read from the flat
  * birth_slots vector (same indexing as keep) when it is not NULL, else from
@@ -95,8 +98,11 @@ int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t max_tokens);
  *   kv_indptr  (opt.)   [B+1] exclusive scan of kept + generated
  *   last_page_len (opt.) [B] ((kept + generated - 1) % page_size) + 1, 0 if empty
  *   counts     (opt.)   [B,3] kept, moved, retired
- *   status     (opt.)   device int32, set to 1 if fresh_count or a
- *                       capacity does not match (outputs are then partial)
+ *   status     (opt.)   device int32: 0, or 1 if fresh_count or a capacity
+ *                       does not match (outputs are then partial)
+ * retired, the copy lists and raw_indices / active_positions may be NULL
+ * when retired_capacity, fresh_count and kept_capacity are 0.
+ * Two launches: per-tile counts, then per-tile prefixes and every output.
  * Replaces the CPU numpy/H2D path of OccurrenceState.advance +
  * terminal_slots + ReqToTokenPool.write + ContextDecodeLayout.from_layout,
  * akv/system/sglang/srt/context_system/occurrence.py:47-66,632-767 and
@@ -104,7 +110,7 @@ int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t max_tokens);
  * akv/system/sglang/srt/disaggregation/context_transfer.py:110-128.
  */
 int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets,
-                     int64_t max_tokens, int32_t* table, int64_t row_stride,
+                     int64_t total_tokens, int32_t* table, int64_t row_stride,
                      const int64_t* row_pointers, const int64_t* req_rows,
                      const uint8_t* keep, const int32_t* birth_positions,
                      const int32_t* final_positions, const int32_t* birth_slots,

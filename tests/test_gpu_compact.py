@@ -123,8 +123,8 @@ def test_side_rows_and_edge_requests(device):
     _run(device, w, side_rows=True, generated=[2, 0, 1, 3, 1, 0])
 
 
-def test_many_small_requests_use_the_scan_launch(device):
-    # 5000 requests -> 5000 tiles: beyond the fused-offsets limit
+def test_many_small_requests(device):
+    # 5000 requests of 1-40 tokens: many requests start and end in every tile
     rng = np.random.default_rng(21)
     lengths, spans = [], []
     for _ in range(5000):
@@ -169,3 +169,55 @@ def test_fresh_count_mismatch_sets_status(device):
     tables.compact_rows(inputs, table, req_rows, fresh[:-1], out)
     torch.cuda.synchronize()
     assert out.status.item() == 1
+
+
+def test_requests_denser_than_the_tile_window(device):
+    # one-token requests: past the first tile more than 256 requests touch
+    # each 256-token tile, so tokens find their request in global memory
+    n = 1500
+    w = synth.Workload("one-token", synth.TINY, (1,) * n, ((),) * n, seed=31, table_positions=8,
+                       pool_slots=4 * n + 1)
+    _run(device, w, generated=[int(x) for x in np.random.default_rng(31).integers(0, 3, size=n)])
+
+
+def test_prefix_over_many_tiles(device):
+    # 80 x 64k tokens: 5000+ tiles of 1024 tokens, each summing the
+    # aggregates of up to 5000 earlier tiles
+    rng = np.random.default_rng(41)
+    lengths = tuple([65536] * 80)
+    spans = tuple(((int(a), int(a) + int(rng.integers(1, 5000))),) for a in rng.integers(0, 60000, size=80))
+    w = synth.Workload("many-groups", synth.TINY, lengths, spans, seed=41, table_positions=65536,
+                       pool_slots=3 * sum(lengths) + 1)
+    _run(device, w, generated=[1] * 80)
+
+
+def test_workspace_reused_across_batches(device):
+    """One workspace serves calls of different sizes in a row, including one
+    that ends with status 1."""
+    big = synth.workload("ragged-64")
+    small = synth.Workload("edges", synth.TINY, (50, 4096 + 17, 5), ((), ((100, 900),), ()), seed=12,
+                           table_positions=5000, pool_slots=40000)
+    runs = []
+    for w in (big, small, big):
+        layouts = synth.compile_layouts(w)
+        runs.append((w, layouts, *_setup(device, w, layouts)))
+    shared = tables.allocate_outputs(runs[0][3], device).workspace
+    for i, (w, layouts, slots, inputs, table, req_rows, fresh, row_pointers, side, tails) in enumerate(runs):
+        out = tables.allocate_outputs(inputs, device)
+        out.workspace = shared
+        if i == 1:
+            # a mismatched call first: it sets status 1
+            bad = tables.allocate_outputs(inputs, device)
+            bad.workspace = shared
+            inputs_bad = tables.CompactionInputs(**{**inputs.__dict__, "moved": (inputs.moved[0] + 1,) + inputs.moved[1:]})
+            fresh_bad = torch.cat((fresh, fresh[:1]))
+            bad.copy_src = torch.empty(len(fresh_bad), dtype=torch.int32, device=device)
+            bad.copy_dst = torch.empty_like(bad.copy_src)
+            bad.copy_pairs = torch.empty((len(fresh_bad), 2), dtype=torch.int32, device=device)
+            tables.compact_rows(inputs_bad, table.clone(), req_rows, fresh_bad, bad)
+            torch.cuda.synchronize()
+            assert bad.status.item() == 1
+        tables.compact_rows(inputs, table, req_rows, fresh, out)
+        torch.cuda.synchronize()
+        rows_after = [table[r].cpu().numpy() for r in req_rows.cpu().numpy()]
+        _check(w, layouts, slots, out, rows_after, tails, [0] * w.n_requests)
