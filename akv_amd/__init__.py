@@ -6,10 +6,14 @@ A drop-in for the KV-cache hot path of thu-nics/AKV:
   K-tail / V move (HIP kernel, bit-exact with the reference arithmetic);
 * ``akv_amd.tables.compact_rows`` -- batched page-table compaction: terminal
   request rows, freed slots, copy lists, decode layout and compacted rows;
-* ``akv_amd.page_table`` -- decode indices, window lengths, indptr rebuild,
-  side-row scatter and the ``ContextDecodeRegistry`` / ``ContextDecodeLayout``
-  interfaces;
+* ``akv_amd.page_table`` -- decode indices, window lengths, indptr rebuild
+  and side-row scatter over the reference registry's rows;
+* ``akv_amd.context_attention.extend_attention_fwd`` -- prefill attention
+  over the compacted rows with context positions;
 * ``akv_amd.plan.compile_context_layout`` -- the host event compiler.
+
+The reference's own host classes (model binding, decode registry, prefill
+metadata, P -> D transfer planning) call these entry points unchanged.
 
 All device work is in ``libakv_amd.so`` (C ABI: ``include/akv_amd.h``),
 built by ``python -m akv_amd.build``.  There is no CPU fallback.

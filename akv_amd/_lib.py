@@ -56,6 +56,10 @@ _SIGNATURES = {
         c_int32,
         [_P, _P, c_int32, _P, c_int32, _P, c_int32, c_int64, _P],
     ),
+    "akv_write_extend_rows": (
+        c_int32,
+        [_P, c_int64, _P, _P, c_int32, _P, c_int32, _P, _P, _P, c_int32, _P, c_int32, c_int32, _P],
+    ),
     "akv_decode_attention_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int64]),
     "akv_decode_attention": (
         c_int32,

@@ -1,189 +1,20 @@
-"""Prefill context attention over occurrence metadata (host side).
+"""Prefill context attention (host side of ``akv_context_attention``).
 
-Mirrors ``ContextSequence`` / ``ContextAttentionPlan`` /
-``ContextAttentionMetadata`` of
-``akv/system/sglang/srt/layers/attention/context_backend.py:24-251`` (same
-fields, packing, validation and messages) and the extend-attention entry
-with context positions (``akv/system/sglang.patch:106-237``).  The device
-work is ``akv_context_attention`` in ``libakv_amd.so``; there is no other
-path.
+``extend_attention_fwd`` is the drop-in for the extend-attention entry with
+context positions (``akv/system/sglang.patch:106-237``): same arguments,
+checks and messages.  The reference's prefill metadata builder
+(``context_backend.py:24-251``) passes it qo/kv indptrs, the bound prefix
+slots and the query / key positions unchanged.  The device work is
+``akv_context_attention`` in ``libakv_amd.so``; there is no other path.
 """
 
 from __future__ import annotations
-
-from collections.abc import Sequence
-from dataclasses import dataclass, field
 
 import numpy as np
 import torch
 
 from . import _lib
 from .ops import _on_device, current_stream_handle
-
-
-def _np(x):
-    return x.numpy() if isinstance(x, torch.Tensor) else np.asarray(x)
-
-
-@dataclass(frozen=True)
-class ContextSequence:
-    """One request's query segments and their visible prefixes (``CB:24-89``)."""
-
-    occurrence_count: int
-    query_lengths: tuple
-    prefix_offsets: np.ndarray
-    prefix_occurrences: np.ndarray
-    query_positions: np.ndarray
-    prefix_positions: np.ndarray
-
-    @classmethod
-    def from_window(cls, window) -> ContextSequence:
-        """Convert one validated occurrence window, keeping query order.
-
-        ``window`` carries ``segment_query_starts/ends``,
-        ``occurrence_raw_tokens``, ``occurrence_positions``,
-        ``birth_occurrences``, ``segment_key_occurrences`` and
-        ``segment_key_offsets`` (``OccurrenceWindow``, ``CS/occurrence.py:84-111``).
-        """
-        starts = _np(window.segment_query_starts)
-        ends = _np(window.segment_query_ends)
-        if len(starts) == 0 or np.any(ends <= starts):
-            raise ValueError("Context attention needs nonempty query segments")
-        if not np.array_equal(ends[:-1], starts[1:]):
-            raise ValueError("Context attention query segments must be contiguous")
-        raw = _np(window.occurrence_raw_tokens)
-        positions = _np(window.occurrence_positions)
-        birth = _np(window.birth_occurrences)
-        keys = _np(window.segment_key_occurrences)
-        key_offsets = _np(window.segment_key_offsets)
-        prefixes, offsets = [], [0]
-        for start, end, a, b in zip(starts, ends, key_offsets[:-1], key_offsets[1:]):
-            selected = keys[a:b]
-            count = int(end - start)
-            if len(selected) < count or not np.array_equal(selected[-count:], birth[start:end]):
-                raise ValueError("Context segment must end in its ordered birth KV")
-            prefix = selected[:-count]
-            if np.any(raw[prefix] >= start):
-                raise ValueError("Context prefix cannot read an uncomputed query")
-            prefixes.append(prefix)
-            offsets.append(offsets[-1] + len(prefix))
-        prefix = np.concatenate(prefixes).astype(np.int64, copy=False)
-        return cls(
-            len(raw),
-            tuple(int(n) for n in ends - starts),
-            np.asarray(offsets, dtype=np.int64),
-            prefix,
-            positions[birth[starts[0] : ends[-1]]].astype(np.int64),
-            positions[prefix].astype(np.int64),
-        )
-
-    @classmethod
-    def ordinary(cls, prefix_length: int, query_length: int) -> ContextSequence:
-        """An ordinary request: ordered prefix slots, then its query write slots."""
-        if prefix_length < 0 or query_length < 1:
-            raise ValueError("Invalid ordinary prefix/query lengths")
-        prefix = np.arange(prefix_length, dtype=np.int64)
-        return cls(
-            prefix_length + query_length,
-            (query_length,),
-            np.asarray([0, prefix_length], dtype=np.int64),
-            prefix,
-            np.arange(prefix_length, prefix_length + query_length, dtype=np.int64),
-            prefix,
-        )
-
-
-@dataclass(frozen=True)
-class ContextAttentionPlan:
-    """One packed int64 transfer of all segment metadata (``CB:91-165``)."""
-
-    packed: torch.Tensor
-    field_ranges: tuple
-    query_lengths: tuple
-    occurrence_count: int
-
-    @classmethod
-    def merge(cls, sequences: Sequence[ContextSequence]) -> ContextAttentionPlan:
-        if not sequences:
-            raise ValueError("Context attention batch cannot be empty")
-        q_lengths, kv_lengths, occurrences, q_pos, kv_pos = [], [], [], [], []
-        base = 0
-        for seq in sequences:
-            q_lengths.extend(seq.query_lengths)
-            kv_lengths.append(np.diff(seq.prefix_offsets))
-            occurrences.append(seq.prefix_occurrences + base)
-            q_pos.append(seq.query_positions)
-            kv_pos.append(seq.prefix_positions)
-            base += seq.occurrence_count
-        fields = (
-            np.r_[0, np.cumsum(q_lengths, dtype=np.int64)],
-            np.r_[0, np.cumsum(np.concatenate(kv_lengths), dtype=np.int64)],
-            np.concatenate(occurrences).astype(np.int64),
-            np.concatenate(q_pos).astype(np.int64),
-            np.concatenate(kv_pos).astype(np.int64),
-        )
-        # fields start on 16-byte boundaries; the ranges exclude the padding
-        offsets = np.r_[0, np.cumsum([(len(f) + 1) // 2 * 2 for f in fields])]
-        packed = np.zeros(int(offsets[-1]), dtype=np.int64)
-        ranges = tuple((int(s), int(s) + len(f)) for s, f in zip(offsets, fields))
-        for f, (s, e) in zip(fields, ranges):
-            packed[s:e] = f
-        return cls(torch.from_numpy(packed), ranges, tuple(q_lengths), base)
-
-    def bind(self, occurrence_slots: torch.Tensor) -> ContextAttentionMetadata:
-        """Bind physical slots (one per batch occurrence) to the prefixes."""
-        if (
-            occurrence_slots.ndim != 1
-            or occurrence_slots.numel() != self.occurrence_count
-            or occurrence_slots.dtype not in (torch.int32, torch.int64)
-        ):
-            raise ValueError("Physical slot binding must cover all batch occurrences")
-        # one staged copy from pageable memory (a fresh pinned buffer per call
-        # costs more than the copy of this size)
-        packed = self.packed.to(device=occurrence_slots.device, non_blocking=True)
-        qo, kv, occurrences, q_positions, kv_positions = [packed[a:b] for a, b in self.field_ranges]
-        return ContextAttentionMetadata(
-            qo,
-            kv,
-            occurrence_slots.index_select(0, occurrences),
-            q_positions,
-            kv_positions,
-            self.query_lengths,
-            sum(self.query_lengths),
-            max(self.query_lengths),
-            tuple(self.packed[a:b].numpy() for a, b in self.field_ranges),
-        )
-
-
-@dataclass(frozen=True)
-class ContextAttentionMetadata:
-    qo_indptr: torch.Tensor
-    kv_indptr: torch.Tensor
-    kv_indices: torch.Tensor
-    query_positions: torch.Tensor
-    kv_positions: torch.Tensor
-    query_lengths: tuple
-    query_count: int
-    max_query_length: int
-    cpu_fields: tuple = ()
-    native_plans: dict = field(default_factory=dict, compare=False, repr=False)
-
-    def forward(self, kernel, q, k, v, output, k_pool, v_pool, **kwargs):
-        """One extend launch, after this layer's KV writes and copy-on-write."""
-        if kwargs.get("page_size", 1) != 1:
-            raise ValueError("Context attention requires page_size=1")
-        if self.query_count != q.shape[0]:
-            raise ValueError("Context query metadata does not cover model output")
-        kernel(
-            q, k, v, output, k_pool, v_pool,
-            self.qo_indptr, self.kv_indptr, self.kv_indices,
-            None, True, None, self.max_query_length, 1.0, 1.0,
-            context_q_positions=self.query_positions,
-            context_kv_positions=self.kv_positions,
-            extend_seq_lens_cpu=self.query_lengths,
-            **kwargs,
-        )
-        return output
 
 
 _INDEX = {torch.int32: _lib.AKV_I32, torch.int64: _lib.AKV_I64}
@@ -202,8 +33,12 @@ def extend_attention_fwd(q_extend, k_extend, v_extend, o_extend, k_buffer, v_buf
     ``k_extend``/``v_extend`` ``[Nq, Hkv, D]`` (this forward's K/V),
     ``k_buffer``/``v_buffer`` the layer's pool ``[slots, Hkv, D]``; prefix rows
     ``kv_indices[kv_indptr[s]:kv_indptr[s+1]]``; queries causal over their own
-    keys.  Supported: bf16, head_dim 64/128, causal, no custom mask, no logit
-    cap, unit K/V scales; anything else raises ``ValueError``.
+    keys.  Supported: bf16 inputs, bf16 or f32 output, head_dim 64 or 128,
+    a GQA group (q heads per KV head) that divides 128 (1, 2, 4, ..., 128;
+    e.g. 28 q heads over 4 KV heads is rejected), row strides that are
+    multiples of 8 elements, causal, no custom mask, no logit cap, unit K/V
+    scales; anything else raises ``ValueError``.  The reference's Triton
+    kernel accepts any group and head dim; these are this kernel's limits.
     """
     use_context_positions = context_q_positions is not None
     if use_context_positions != (context_kv_positions is not None):

@@ -5,6 +5,8 @@
 //   akv_window_lengths   context_window_lengths (context_page_table.py:7-31)
 //   akv_build_indptr     kv_indptr[1:] = cumsum(seq_lens) (akv/system/sglang.patch:2266-2268)
 //   akv_write_row_slots  write_row_slots (akv/system/sglang/kernels/ops/memory/context_rows.py:7-15)
+//   akv_write_extend_rows write_req_to_token_pool_triton with RowPointers
+//                        (akv/system/sglang.patch:238-278, caller sglang.patch:4066-4090)
 //
 // The reference walks each request with one program in 256-token steps; here
 // every request gets several workgroups that stride over its range, so one
@@ -12,6 +14,8 @@
 // int64[6] = (raw_ids_ptr, positions_ptr, prompt_len, active, next_pos,
 // row_ptr); a zero raw_ids_ptr marks an ordinary request.
 #include "common.h"
+
+extern "C" __device__ long long __ockl_wfred_add_i64(long long);
 
 namespace akv {
 namespace {
@@ -182,6 +186,49 @@ __global__ void __launch_bounds__(256) write_row_slots_kernel(const RowSlotArgs 
   p[column] = static_cast<int32_t>(load_index(a.values, a.values64, i));
 }
 
+// Extend write: per request b, row[0, pre) = prefix_b[0, pre) and
+// row[pre, seq) = out_cache_loc[start_b + (0 .. seq - pre)), start_b the
+// exclusive prefix of extend_lens.  Grid (kExtendSlices, B): each workgroup
+// writes one slice of its request's row.
+constexpr int kExtendSlices = 8;
+
+struct ExtendArgs {
+  int32_t* table;
+  int64_t row_stride;
+  const int64_t* row_pointers;
+  const void* req_rows;
+  const int64_t* prefix_ptrs;
+  const void* pre_lens;
+  const void* seq_lens;
+  const void* extend_lens;
+  const void* out_cache_loc;
+  bool rows64, prefix64, lens64, loc64;
+};
+
+__global__ void __launch_bounds__(256) write_extend_rows_kernel(const ExtendArgs a) {
+  const int b = blockIdx.y;
+  // start of this request's new slots: sum of the earlier extend lengths
+  int64_t before = 0;
+  for (int i = threadIdx.x; i < b; i += 256) before += load_index(a.extend_lens, a.lens64, i);
+  before = __ockl_wfred_add_i64(before);
+  __shared__ int64_t part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = before;
+  __syncthreads();
+  const int64_t start = part[0] + part[1] + part[2] + part[3];
+  const int64_t r = load_index(a.req_rows, a.rows64, b);
+  int32_t* row = a.row_pointers ? reinterpret_cast<int32_t*>(a.row_pointers[r]) : a.table + r * a.row_stride;
+  const int64_t pre = load_index(a.pre_lens, a.lens64, b);
+  const int64_t seq = load_index(a.seq_lens, a.lens64, b);
+  const void* prefix = reinterpret_cast<const void*>(a.prefix_ptrs[b]);
+  const int64_t slice = ((seq + kExtendSlices - 1) / kExtendSlices + 255) / 256 * 256;
+  const int64_t lo = blockIdx.x * slice;
+  const int64_t hi = lo + slice < seq ? lo + slice : seq;
+  for (int64_t j = lo + threadIdx.x; j < hi; j += 256) {
+    const int64_t v = j < pre ? load_index(prefix, a.prefix64, j) : load_index(a.out_cache_loc, a.loc64, start + j - pre);
+    row[j] = static_cast<int32_t>(v);
+  }
+}
+
 }  // namespace
 }  // namespace akv
 
@@ -294,4 +341,39 @@ extern "C" int akv_write_row_slots(const int64_t* pointers, const void* rows, in
   if (blocks > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_write_row_slots: too many entries");
   hipLaunchKernelGGL(write_row_slots_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream), a);
   return check_launch("akv_write_row_slots");
+}
+
+extern "C" int akv_write_extend_rows(int32_t* table, int64_t row_stride, const int64_t* row_pointers,
+                                     const void* req_rows, int32_t rows_dtype, const int64_t* prefix_ptrs,
+                                     int32_t prefix_dtype, const void* pre_lens, const void* seq_lens,
+                                     const void* extend_lens, int32_t lens_dtype, const void* out_cache_loc,
+                                     int32_t loc_dtype, int32_t n_requests, void* stream) {
+  using namespace akv;
+  if (n_requests < 0) return fail(AKV_EINVAL, "akv_write_extend_rows: negative batch size");
+  if (n_requests == 0) return AKV_OK;
+  if (n_requests > 65535)
+    return fail(AKV_EINVAL, "akv_write_extend_rows: batch of %d requests exceeds one launch", n_requests);
+  if ((!table && !row_pointers) || !req_rows || !prefix_ptrs || !pre_lens || !seq_lens || !extend_lens ||
+      !out_cache_loc)
+    return fail(AKV_EINVAL, "akv_write_extend_rows: null device pointer");
+  if (!valid_index_dtype(rows_dtype) || !valid_index_dtype(prefix_dtype) || !valid_index_dtype(lens_dtype) ||
+      !valid_index_dtype(loc_dtype))
+    return fail(AKV_EINVAL, "akv_write_extend_rows: index vectors must be int32 or int64");
+  ExtendArgs a{};
+  a.table = table;
+  a.row_stride = row_stride;
+  a.row_pointers = row_pointers;
+  a.req_rows = req_rows;
+  a.prefix_ptrs = prefix_ptrs;
+  a.pre_lens = pre_lens;
+  a.seq_lens = seq_lens;
+  a.extend_lens = extend_lens;
+  a.out_cache_loc = out_cache_loc;
+  a.rows64 = rows_dtype == AKV_I64;
+  a.prefix64 = prefix_dtype == AKV_I64;
+  a.lens64 = lens_dtype == AKV_I64;
+  a.loc64 = loc_dtype == AKV_I64;
+  hipLaunchKernelGGL(write_extend_rows_kernel, dim3(kExtendSlices, static_cast<unsigned>(n_requests)), dim3(256), 0,
+                     as_stream(stream), a);
+  return check_launch("akv_write_extend_rows");
 }

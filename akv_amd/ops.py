@@ -8,8 +8,6 @@ current HIP stream of the KV device.  No allocation, no device-to-host read,
 no synchronisation.
 """
 
-from dataclasses import dataclass
-
 import torch
 
 from . import _lib
@@ -162,42 +160,3 @@ def reposition_kv_layers(
             current_stream_handle(k_layout.device),
         )
     _lib.check(rc, "akv_reposition_kv_layers")
-
-
-@dataclass(frozen=True)
-class ContextLayerCopy:
-    """One layer's fresh destinations, bound before model execution.
-
-    Mirrors ``ContextLayerCopy``
-    (``akv/system/sglang/srt/layers/attention/context_backend.py:302-341``):
-    ``apply`` runs the single-layer Reposition of this forward's copies.
-    """
-
-    k_data_ptrs: torch.Tensor
-    v_data_ptrs: torch.Tensor
-    k_layout: torch.Tensor
-    v_layout: torch.Tensor
-    source_slots: torch.Tensor
-    destination_slots: torch.Tensor
-    position_pairs: torch.Tensor
-    cos_sin_cache: torch.Tensor
-    is_neox_style: bool
-    skip_unmapped: bool = False
-    rotary_dim: int | None = None
-
-    def apply(self):
-        if len(self.k_data_ptrs) != 1 or len(self.v_data_ptrs) != 1:
-            raise ValueError("Per-layer birth copies must address exactly one layer")
-        reposition_kv_layers(
-            self.k_data_ptrs,
-            self.v_data_ptrs,
-            self.k_layout,
-            self.v_layout,
-            self.source_slots,
-            self.destination_slots,
-            self.position_pairs,
-            self.cos_sin_cache,
-            is_neox_style=self.is_neox_style,
-            skip_unmapped=self.skip_unmapped,
-            rotary_dim=self.rotary_dim,
-        )

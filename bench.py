@@ -285,19 +285,24 @@ def decode_consumer_config(device, flush):
                         birth_slots=torch.from_numpy(np.concatenate(slots.birth_rows)).to(device))
     pool = synth.make_pool(model, w.pool_slots, device, seed=9, generate_on_device=True)
 
-    class _T:
-        page_size, defer_read_translate, is_translating = 1, False, False
-        req_to_token = table
-
-    registry = page_table.ContextDecodeRegistry(_T(), pool=None)
+    # registry rows (the reference registry's row format) straight from the
+    # compaction outputs: raw indices and positions of the active versions
     kept_off = np.concatenate(([0], np.cumsum(inputs.kept)))
-    registry.rows[rows] = torch.tensor(
+    registry = torch.tensor(
         [(out.raw_indices.data_ptr() + 4 * int(kept_off[b]), out.active_positions.data_ptr() + 4 * int(kept_off[b]),
           n, inputs.kept[b], layouts[b].next_position, 0) for b in range(B)], dtype=torch.int64).to(device)
     seq = torch.tensor([k + 1 for k in inputs.kept], dtype=torch.int64, device=device)
     win_indptr = torch.zeros(B + 1, dtype=torch.int32, device=device)
     win_idx = torch.zeros(B * 129, dtype=torch.int32, device=device)
-    registry.fill_window(rows, seq, win_indptr, 128, win_idx)
+    win_len = torch.empty_like(seq)
+    win_start = torch.empty_like(seq)
+
+    def meta_window():
+        page_table.context_window_lengths(registry, rows, seq, win_len, 128, starts=win_start)
+        page_table.build_indptr(win_len, win_indptr)
+        page_table.context_decode_indices(registry, table, rows, win_len, win_indptr, win_idx, starts=win_start)
+
+    meta_window()
     q = torch.randn((B, 64, 64), device=device).to(torch.bfloat16)
     sinks = torch.randn(64, device=device)
     o = torch.empty((B, 64, 64), dtype=torch.bfloat16, device=device)
@@ -319,14 +324,11 @@ def decode_consumer_config(device, flush):
 
     def meta_full():
         page_table.build_indptr(seq, meta_indptr)
-        registry.fill(rows, seq, meta_indptr, meta_idx)
-
-    def meta_window():
-        registry.fill_window(rows, seq, win_indptr, 128, win_idx)
+        page_table.context_decode_indices(registry, table, rows, seq, meta_indptr, meta_idx)
 
     meta_full()
     if not (torch.equal(meta_indptr, out.kv_indptr.to(torch.int32)) and torch.equal(meta_idx, out.kv_indices)):
-        raise RuntimeError("decode metadata from the registry disagrees with the compaction's kv_indices")
+        raise RuntimeError("decode read indices disagree with the compaction's kv_indices")
     warm_meta_full, cold_meta_full = _time_steps(meta_full, 50, 5, 20, flush)
     warm_meta_win, cold_meta_win = _time_steps(meta_window, 50, 5, 20, flush)
     warm_full, cold_full = _time_steps(full, 20, 5, 20, flush)

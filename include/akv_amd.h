@@ -215,6 +215,26 @@ int akv_write_row_slots(const int64_t* pointers, const void* rows,
                         int32_t values_dtype, int64_t n, void* stream);
 
 /*
+ * Extend write of request rows.  For request b (table row r =
+ * req_rows[b]; its row is row_pointers[r] when row_pointers != NULL, else
+ * table + r * row_stride):
+ *   row[0, pre_lens[b])             = prefix_b[0, pre_lens[b]),
+ *   row[pre_lens[b], seq_lens[b])   = out_cache_loc[s_b, s_b + seq - pre),
+ * prefix_b the device array at address prefix_ptrs[b] (prefix_dtype), s_b
+ * the sum of extend_lens[0, b).  Values are stored as int32.
+ * Replaces write_req_to_token_pool_triton with RowPointers,
+ * akv/system/sglang.patch:238-278 (called from write_cache_indices,
+ * sglang.patch:4066-4090).
+ */
+int akv_write_extend_rows(int32_t* table, int64_t row_stride,
+                          const int64_t* row_pointers, const void* req_rows,
+                          int32_t rows_dtype, const int64_t* prefix_ptrs,
+                          int32_t prefix_dtype, const void* pre_lens,
+                          const void* seq_lens, const void* extend_lens,
+                          int32_t lens_dtype, const void* out_cache_loc,
+                          int32_t loc_dtype, int32_t n_requests, void* stream);
+
+/*
  * Device bytes of the split-K scratch of akv_decode_attention.
  */
 int64_t akv_decode_attention_workspace_bytes(int32_t n_requests,

@@ -60,6 +60,11 @@ def test_validation_rejects_before_any_device_work(lib):
     assert lib.akv_bind_occurrences(*zeros(lib.akv_bind_occurrences, a0=2, a2=9)) == _lib.AKV_EINVAL
     assert "null device pointer" in _lib.last_error()
     assert lib.akv_bind_workspace_bytes(4, 100000) > 0
+    # extend write: n_requests is argument 13
+    assert lib.akv_write_extend_rows(*zeros(lib.akv_write_extend_rows, a13=-1)) == _lib.AKV_EINVAL
+    assert lib.akv_write_extend_rows(*zeros(lib.akv_write_extend_rows)) == 0  # empty batch
+    assert lib.akv_write_extend_rows(*zeros(lib.akv_write_extend_rows, a13=3)) == _lib.AKV_EINVAL
+    assert "null device pointer" in _lib.last_error()
     assert lib.akv_context_attention(*zeros(lib.akv_context_attention, a15=1, a17=1, a18=64, a34=4)) == _lib.AKV_EINVAL
     # prefix indices without K/V pools: rejected instead of faulting on the
     # null pool (addresses are never dereferenced on this path)

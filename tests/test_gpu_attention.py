@@ -7,9 +7,11 @@ import numpy as np
 import pytest
 import torch
 
-from akv_amd import attention, ops, page_table, synth, tables
+from akv_amd import attention, ops, synth, tables
 from oracle import attention as oat
 from oracle import occurrence as occ
+
+from harness import window_indices
 
 pytestmark = pytest.mark.gpu
 
@@ -77,20 +79,15 @@ def test_gpt_oss_decode_after_drop_and_reposition(device):
                              out.copy_pairs, rope)
 
     # registry rows straight from the compaction outputs
-    class _T:
-        page_size, defer_read_translate, is_translating = 1, False, False
-        req_to_token = table
-
-    registry = page_table.ContextDecodeRegistry(_T(), pool=None)
     kept_off = np.concatenate(([0], np.cumsum(inputs.kept)))
-    registry.rows[rows] = torch.tensor(
+    registry = torch.tensor(
         [(out.raw_indices.data_ptr() + 4 * int(kept_off[b]), out.active_positions.data_ptr() + 4 * int(kept_off[b]),
           n, inputs.kept[b], layouts[b].next_position, 0) for b in range(B)], dtype=torch.int64).to(device)
     seq = torch.tensor([k + 1 for k in inputs.kept], dtype=torch.int64, device=device)
     window = 128
     win_indptr = torch.zeros(B + 1, dtype=torch.int32, device=device)
     win_idx = torch.zeros(B * (window + 1), dtype=torch.int32, device=device)
-    registry.fill_window(rows, seq, win_indptr, window, win_idx)
+    window_indices(registry, table, rows, seq, window, win_indptr, win_idx)
 
     g = torch.Generator().manual_seed(5)
     q = torch.randn((B, 64, 64), generator=g).to(torch.bfloat16).to(device)

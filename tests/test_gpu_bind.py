@@ -7,7 +7,6 @@ import numpy as np
 import pytest
 import torch
 
-from akv_amd import context_attention as ca
 from akv_amd import occurrence as ow
 from akv_amd import ops, plan
 from akv_amd.rope import make_table
@@ -15,6 +14,7 @@ from oracle import attention as oat
 from oracle import events as ev
 from oracle import occurrence as occ
 
+from harness import attention_metadata, prefill_forward, window_segments
 from test_occurrence_window import _program, _torch_layout
 
 pytestmark = pytest.mark.gpu
@@ -107,15 +107,15 @@ def test_prefill_reads_bound_occurrences_after_reposition(device):
     ptr_k = torch.tensor([k_pool.data_ptr()], dtype=torch.uint64, device=device)
     ptr_v = torch.tensor([v_pool.data_ptr()], dtype=torch.uint64, device=device)
     ops.reposition_kv_layers(ptr_k, ptr_v, k_pool, v_pool, out.copy_src, out.copy_dst, out.copy_pairs, table_rope)
-    seq = ca.ContextSequence.from_window(window)
-    meta = ca.ContextAttentionPlan.merge([seq]).bind(out.occurrence_slots.long())
+    meta = attention_metadata([window_segments(window)], out.occurrence_slots.long())
     q = torch.randn((n, hq, d), generator=g).to(torch.bfloat16).to(device)
     o = torch.empty_like(q)
-    meta.forward(ca.extend_attention_fwd, q, k_ext, v_ext, o, k_pool, v_pool, sliding_window_size=-1)
+    prefill_forward(meta, q, k_ext, v_ext, o, k_pool, v_pool, sliding_window_size=-1)
     torch.cuda.synchronize()
-    qo, kv, occ_ids, qpos, kpos = meta.cpu_fields
+    c = meta.cpu
     want_slots = occ.advance_final_forward(ref, occ.plan_final_forward(ref, visible), birth, fresh)["occurrence_slots"]
     f32 = lambda t: t.float().cpu().numpy()
-    want = oat.context_attention(f32(q), f32(k_ext), f32(v_ext), f32(k_pool), f32(v_pool), qo, kv,
-                                 want_slots[occ_ids], d ** -0.5, q_positions=qpos, kv_positions=kpos)
+    want = oat.context_attention(f32(q), f32(k_ext), f32(v_ext), f32(k_pool), f32(v_pool), c.qo_indptr, c.kv_indptr,
+                                 want_slots[c.occurrences], d ** -0.5, q_positions=c.query_positions,
+                                 kv_positions=c.kv_positions)
     assert np.abs(f32(o) - want).max() <= 2e-2

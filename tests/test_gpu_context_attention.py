@@ -1,8 +1,8 @@
 """GPU parity of the prefill context attention (MFMA) against the float64
 oracle: ragged segments, empty and long prefixes, GQA groups 8 and 4, head
 dims 64 and 128, position-based sliding windows over positions with holes,
-the native (position-free) window, sinks, bf16 and f32 outputs; and the
-metadata path (ContextSequence -> plan -> bind -> forward)."""
+the native (position-free) window, sinks, bf16 and f32 outputs; and batch
+metadata of plain requests bound to physical slots."""
 
 import numpy as np
 import pytest
@@ -10,6 +10,8 @@ import torch
 
 from akv_amd import context_attention as ca
 from oracle import attention as oat
+
+from harness import attention_metadata, plain_segments, prefill_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -151,28 +153,29 @@ def test_group_sizes(device, d, hq, hkv):
     assert np.abs(got - want).max() <= TOL
 
 
-def test_metadata_path_ordinary_sequences(device):
-    """ContextSequence.ordinary -> ContextAttentionPlan.merge/bind -> forward."""
+def test_metadata_from_plain_requests(device):
+    """Batch metadata of plain requests (prefix, then queries) bound to
+    permuted physical slots -> one launch."""
     hq, hkv, d = 64, 8, 64
-    seqs = [ca.ContextSequence.ordinary(37, 20), ca.ContextSequence.ordinary(0, 70),
-            ca.ContextSequence.ordinary(300, 1)]
-    plan = ca.ContextAttentionPlan.merge(seqs)
+    requests = [plain_segments(37, 20), plain_segments(0, 70), plain_segments(300, 1)]
+    n_occ = sum(r.occurrences for r in requests)
     rng = np.random.default_rng(0)
-    slots = torch.from_numpy(rng.permutation(np.arange(1, 1 + plan.occurrence_count)).astype(np.int64)).to(device)
-    meta = plan.bind(slots)
+    slots = torch.from_numpy(rng.permutation(np.arange(1, 1 + n_occ)).astype(np.int64)).to(device)
+    meta = attention_metadata(requests, slots)
     g = torch.Generator().manual_seed(2)
     nq = meta.query_count
     q = torch.randn((nq, hq, d), generator=g).to(torch.bfloat16).to(device)
     ke = torch.randn((nq, hkv, d), generator=g).to(torch.bfloat16).to(device)
     ve = torch.randn((nq, hkv, d), generator=g).to(torch.bfloat16).to(device)
-    pool_k = torch.randn((plan.occurrence_count + 1, hkv, d), generator=g).to(torch.bfloat16).to(device)
-    pool_v = torch.randn((plan.occurrence_count + 1, hkv, d), generator=g).to(torch.bfloat16).to(device)
+    pool_k = torch.randn((n_occ + 1, hkv, d), generator=g).to(torch.bfloat16).to(device)
+    pool_v = torch.randn((n_occ + 1, hkv, d), generator=g).to(torch.bfloat16).to(device)
     out = torch.empty_like(q)
-    meta.forward(ca.extend_attention_fwd, q, ke, ve, out, pool_k, pool_v, sliding_window_size=-1)
+    prefill_forward(meta, q, ke, ve, out, pool_k, pool_v, sliding_window_size=-1)
     torch.cuda.synchronize()
-    qo, kv, occ, qpos, kpos = meta.cpu_fields
-    want = oat.context_attention(_f32(q), _f32(ke), _f32(ve), _f32(pool_k), _f32(pool_v), qo, kv,
-                                 slots.cpu().numpy()[occ], d ** -0.5, q_positions=qpos, kv_positions=kpos)
+    c = meta.cpu
+    want = oat.context_attention(_f32(q), _f32(ke), _f32(ve), _f32(pool_k), _f32(pool_v), c.qo_indptr, c.kv_indptr,
+                                 slots.cpu().numpy()[c.occurrences], d ** -0.5, q_positions=c.query_positions,
+                                 kv_positions=c.kv_positions)
     assert np.abs(_f32(out) - want).max() <= TOL
 
 

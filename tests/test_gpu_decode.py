@@ -1,4 +1,6 @@
-"""GPU parity of the decode-metadata kernels and the registry interface."""
+"""GPU parity of the decode-metadata kernels (read indices, window lengths,
+indptr rebuild, side-row scatter), driven the way a decode registry drives
+them: one int64 row per request pointing at its final active versions."""
 
 import numpy as np
 import pytest
@@ -9,30 +11,18 @@ from akv_amd import synth, tables
 from oracle import decode as dec
 from oracle import occurrence as occ
 
+from harness import DecodeRows, dense_indices, window_indices
+
 pytestmark = pytest.mark.gpu
 
 
-class _Translator:
-    page_size = 1
-    defer_read_translate = False
-    is_translating = False
-
-    def __init__(self, req_to_token):
-        self.req_to_token = req_to_token
-
-
-class _Req:
-    def __init__(self, layout, row):
-        self.context_program = None if layout is None else type("P", (), {"layout": layout})()
-        self.context_decode_layout = None
-        self.kv = type("K", (), {"req_pool_idx": row})()
-
-
 def _batch(device, seed=0, batch=24):
+    """Requests in table rows 2 .. batch+1: a quarter ordinary, the rest after
+    a final forward (terminal row), each with a few generated tokens."""
     rng = np.random.default_rng(seed)
     width = 3000
     table = np.full((batch + 4, width), -3, dtype=np.int32)
-    reqs, raw_lengths, expect = [], [], []
+    entries, seq, expect = [], [], []
     for b in range(batch):
         row = b + 2
         n = int(rng.integers(20, 2500))
@@ -40,8 +30,8 @@ def _batch(device, seed=0, batch=24):
         slots = rng.integers(1, 10**7, size=n + gen).astype(np.int32)
         if rng.random() < 0.25:
             table[row, : n + gen] = slots
-            reqs.append(_Req(None, row))
-            raw_lengths.append(n + gen)
+            entries.append((row, None))
+            seq.append(n + gen)
             expect.append((None, slots.copy(), gen))
             continue
         k = int(rng.integers(1, 4))
@@ -53,53 +43,39 @@ def _batch(device, seed=0, batch=24):
                              rng.integers(1, 10**7, size=int(moved.sum())))
         table[row, :n] = cf["terminal_row"]
         table[row, n : n + gen] = slots[n:]
-        reqs.append(_Req(lay, row))
-        raw_lengths.append(n + gen)
+        entries.append((row, lay))
+        seq.append(int(lay.keep_mask.sum()) + gen)
         expect.append((lay, np.concatenate((cf["active_slots"], slots[n:])), gen))
-    return torch.from_numpy(table).to(device), reqs, raw_lengths, expect
+    table = torch.from_numpy(table).to(device)
+    reg = DecodeRows.from_layouts(batch + 4, entries, device)
+    row_ids = torch.tensor([r for r, _ in entries], dtype=torch.int64, device=device)
+    return table, reg, row_ids, np.asarray(seq, dtype=np.int64), expect
 
 
-def test_registry_fill_matches_compacted_rows(device):
-    table, reqs, raw_lengths, expect = _batch(device)
-    registry = pt.ContextDecodeRegistry(_Translator(table), pool=None)
-    row_ids = torch.tensor([r.kv.req_pool_idx for r in reqs], dtype=torch.int64, device=device)
-    lengths, _, positions, refs = registry.bind_batch(reqs, raw_lengths, row_ids)
-    seq = lengths.to(device)
+def test_read_indices_match_compacted_rows(device):
+    table, reg, row_ids, lengths, expect = _batch(device)
+    seq = torch.from_numpy(lengths).to(device)
     for out_dtype in (torch.int32, torch.int64):
-        indptr = torch.empty(len(reqs) + 1, dtype=torch.int32, device=device)
+        indptr = torch.empty(len(lengths) + 1, dtype=torch.int32, device=device)
         pt.build_indptr(seq, indptr)
         out = torch.full((int(lengths.sum()),), -9, dtype=out_dtype, device=device)
-        registry.fill(row_ids, seq, indptr, out)
+        pt.context_decode_indices(reg.rows, table, row_ids, seq, indptr, out)
         torch.cuda.synchronize()
         got = out.cpu().numpy()
         ip = indptr.cpu().numpy()
-        np.testing.assert_array_equal(ip, dec.kv_indptr(lengths.numpy()))
+        np.testing.assert_array_equal(ip, dec.kv_indptr(lengths))
         for b, (_, want, _) in enumerate(expect):
             np.testing.assert_array_equal(got[ip[b] : ip[b + 1]], want)
-    # query positions: next_position + generated - 1
-    for b, (lay, _, gen) in enumerate(expect):
-        if lay is not None:
-            assert int(positions[b]) == lay.next_position + gen - 1
 
 
 @pytest.mark.parametrize("window", [0, 1, 7, 128, 5000])
-def test_fill_window_and_table_match_oracle(device, window):
-    table, reqs, raw_lengths, expect = _batch(device, seed=1)
-    registry = pt.ContextDecodeRegistry(_Translator(table), pool=None)
-    row_ids = torch.tensor([r.kv.req_pool_idx for r in reqs], dtype=torch.int64, device=device)
-    lengths, _, _, refs = registry.bind_batch(reqs, raw_lengths, row_ids)
-    seq = lengths.to(device)
-    reg_np = registry.rows.cpu().numpy()
-    memory = {}
-    for r in reqs:
-        lay = r.context_decode_layout
-        if lay is not None:
-            memory[lay.device_indices.data_ptr()] = lay.raw_indices
-            memory[lay.device_positions.data_ptr()] = lay.positions
-    want_len = dec.window_lengths(reg_np, row_ids.cpu().numpy(), lengths.numpy(), window, memory=memory)
-    indptr_buf = torch.zeros(len(reqs) + 8, dtype=torch.int32, device=device)
+def test_window_and_dense_table_match_oracle(device, window):
+    table, reg, row_ids, lengths, expect = _batch(device, seed=1)
+    seq = torch.from_numpy(lengths).to(device)
+    want_len = dec.window_lengths(reg.rows.cpu().numpy(), row_ids.cpu().numpy(), lengths, window, memory=reg.host)
+    indptr_buf = torch.zeros(len(lengths) + 8, dtype=torch.int32, device=device)
     out = torch.zeros(int(want_len.sum()) + 5, dtype=torch.int64, device=device)
-    indptr, _, got_len, starts = registry.fill_window(row_ids, seq, indptr_buf, window, out)
+    indptr, got_len, _ = window_indices(reg.rows, table, row_ids, seq, window, indptr_buf, out)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(got_len.cpu().numpy(), want_len)
     ip = indptr.cpu().numpy()
@@ -108,8 +84,8 @@ def test_fill_window_and_table_match_oracle(device, window):
         s = int(lengths[b]) - int(want_len[b])
         np.testing.assert_array_equal(out.cpu().numpy()[ip[b] : ip[b + 1]], full[s:])
     # dense page-one table form (FA3 style)
-    dense = torch.full((len(reqs), 3000), -1, dtype=torch.int32, device=device)
-    got = registry.fill_table(row_ids, seq, dense, window=window)
+    dense = torch.full((len(lengths), 3000), -1, dtype=torch.int32, device=device)
+    got = dense_indices(reg.rows, table, row_ids, seq, dense, window=window)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(got.cpu().numpy(), want_len)
     d = dense.cpu().numpy()
@@ -119,20 +95,14 @@ def test_fill_window_and_table_match_oracle(device, window):
 
 
 def test_mapping_translation_and_row_slots(device):
-    table, reqs, raw_lengths, expect = _batch(device, seed=2, batch=6)
+    table, reg, row_ids, lengths, expect = _batch(device, seed=2, batch=6)
     mapping = (torch.arange(10**7, dtype=torch.int64) * 5 + 3).to(device)
-    t = _Translator(table)
-    t.is_translating = True
-    t._full_v2p_table = mapping
-    t._full_page_multiplier = 2
-    registry = pt.ContextDecodeRegistry(t, pool=None)
-    row_ids = torch.tensor([r.kv.req_pool_idx for r in reqs], dtype=torch.int32, device=device)
-    lengths, _, _, _ = registry.bind_batch(reqs, raw_lengths, row_ids)
-    seq = lengths.to(device)
-    indptr = torch.empty(len(reqs) + 1, dtype=torch.int64, device=device)
+    seq = torch.from_numpy(lengths).to(device)
+    indptr = torch.empty(len(lengths) + 1, dtype=torch.int64, device=device)
     pt.build_indptr(seq, indptr)
     out = torch.zeros(int(lengths.sum()), dtype=torch.int64, device=device)
-    registry.fill(row_ids, seq, indptr, out)
+    pt.context_decode_indices(reg.rows, table, row_ids.to(torch.int32), seq, indptr, out, mapping=mapping,
+                              multiplier=2)
     torch.cuda.synchronize()
     ip = indptr.cpu().numpy()
     for b, (_, want, _) in enumerate(expect):
@@ -162,7 +132,7 @@ def test_indptr_and_last_page(device):
 
 
 def test_pipeline_compaction_feeds_registry(device):
-    """compact_rows outputs bind directly as registry rows (no host round trip)."""
+    """compact_rows outputs serve directly as registry rows (no host round trip)."""
     w = synth.workload("ragged-64")
     layouts = synth.compile_layouts(w)
     slots = synth.assign_slots(w, layouts)
@@ -178,19 +148,65 @@ def test_pipeline_compaction_feeds_registry(device):
     gen = torch.ones(w.n_requests, dtype=torch.int32, device=device)
     row_ids = torch.arange(w.n_requests, dtype=torch.int64, device=device)
     tables.compact_rows(inputs, table, row_ids, fresh, out, generated=gen)
-    registry = pt.ContextDecodeRegistry(_Translator(table), pool=None)
     kept_off = np.concatenate(([0], np.cumsum(inputs.kept)))
     rows = []
     for b, lay in enumerate(layouts):
         raw_ptr = out.raw_indices.data_ptr() + 4 * int(kept_off[b])
         pos_ptr = out.active_positions.data_ptr() + 4 * int(kept_off[b])
         rows.append((raw_ptr, pos_ptr, w.lengths[b], inputs.kept[b], lay.next_position, 0))
-    registry.rows[row_ids] = torch.tensor(rows, dtype=torch.int64).to(device)
+    registry = torch.tensor(rows, dtype=torch.int64).to(device)
     seq = torch.tensor([k + 1 for k in inputs.kept], dtype=torch.int64, device=device)
     indptr = torch.empty(w.n_requests + 1, dtype=torch.int32, device=device)
     pt.build_indptr(seq, indptr)
     kv = torch.empty(int(seq.sum()), dtype=torch.int32, device=device)
-    registry.fill(row_ids, seq, indptr, kv)
+    pt.context_decode_indices(registry, table, row_ids, seq, indptr, kv)
     torch.cuda.synchronize()
     assert torch.equal(kv, out.kv_indices)
     assert torch.equal(indptr, out.kv_indptr)
+
+
+@pytest.mark.parametrize("lens_dtype,loc_dtype", [(torch.int64, torch.int64), (torch.int32, torch.int32)])
+def test_extend_write_matches_numpy(device, lens_dtype, loc_dtype):
+    """Extend write of request rows (prefix, then new slots) into table rows
+    and, for some requests, side rows reached through row pointers."""
+    rng = np.random.default_rng(7)
+    pool_rows, width, batch = 12, 5000, 9
+    table = torch.full((pool_rows, width), -4, dtype=torch.int32, device=device)
+    side = {r: torch.full((width,), -6, dtype=torch.int32, device=device) for r in (3, 8)}
+    pointers = torch.tensor([side[r].data_ptr() if r in side else table[r].data_ptr() for r in range(pool_rows)],
+                            dtype=torch.int64, device=device)
+    req_rows = rng.permutation(pool_rows)[:batch]
+    pre = rng.integers(0, 3000, size=batch)
+    pre[0] = 0
+    ext = rng.integers(1, 1500, size=batch)
+    seq = pre + ext
+    prefixes = [torch.from_numpy(rng.integers(1, 10**6, size=max(p, 1))).to(device) for p in pre]
+    loc = rng.integers(1, 10**6, size=int(ext.sum()))
+    args = dict(
+        req_pool_indices=torch.from_numpy(req_rows.astype(np.int64)).to(device),
+        prefix_tensors=torch.tensor([t.data_ptr() for t in prefixes], dtype=torch.int64, device=device),
+        pre_lens=torch.from_numpy(pre).to(lens_dtype).to(device),
+        seq_lens=torch.from_numpy(seq).to(lens_dtype).to(device),
+        extend_lens=torch.from_numpy(ext).to(lens_dtype).to(device),
+        out_cache_loc=torch.from_numpy(loc).to(loc_dtype).to(device))
+    want_table = table.cpu().numpy().copy()
+    want_side = {r: t.cpu().numpy().copy() for r, t in side.items()}
+    start = np.concatenate(([0], np.cumsum(ext)))
+    for b, r in enumerate(req_rows):
+        row = want_side[r] if r in side else want_table[r]
+        row[: pre[b]] = prefixes[b].cpu().numpy()[: pre[b]]
+        row[pre[b] : seq[b]] = loc[start[b] : start[b + 1]]
+    pt.write_req_to_token_pool(table, row_pointers=pointers, **args)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(table.cpu().numpy(), want_table)  # side-row requests leave the table alone
+    for r, t in side.items():
+        np.testing.assert_array_equal(t.cpu().numpy(), want_side[r])
+    # without row pointers every request writes its table row
+    table2 = torch.full((pool_rows, width), -4, dtype=torch.int32, device=device)
+    want2 = table2.cpu().numpy().copy()
+    for b, r in enumerate(req_rows):
+        want2[r, : pre[b]] = prefixes[b].cpu().numpy()[: pre[b]]
+        want2[r, pre[b] : seq[b]] = loc[start[b] : start[b + 1]]
+    pt.write_req_to_token_pool(table2, **args)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(table2.cpu().numpy(), want2)

@@ -7,14 +7,9 @@ import torch
 
 from akv_amd import ops, page_table, synth, tables
 
+from harness import attention_metadata, plain_segments, prefill_forward
+
 pytestmark = pytest.mark.gpu
-
-
-class _T:
-    page_size, defer_read_translate, is_translating = 1, False, False
-
-    def __init__(self, table):
-        self.req_to_token = table
 
 
 def test_graph_replays_match_eager(device):
@@ -33,10 +28,12 @@ def test_graph_replays_match_eager(device):
     gen = torch.ones(1, dtype=torch.int32, device=device)
     pool = synth.make_pool(w.model, w.pool_slots, device, seed=3, generate_on_device=False)
     rope = synth.rope_table(w, device)
-    registry = page_table.ContextDecodeRegistry(_T(table), pool=None)
     kept = int(lay.keep_mask.sum())
-    registry.rows[1] = torch.tensor([out.raw_indices.data_ptr(), out.active_positions.data_ptr(), n, kept,
-                                     lay.next_position, 0], dtype=torch.int64)
+    # registry row 1: the request's final active versions, as compacted
+    registry = torch.zeros((2, 6), dtype=torch.int64)
+    registry[1] = torch.tensor([out.raw_indices.data_ptr(), out.active_positions.data_ptr(), n, kept,
+                                lay.next_position, 0], dtype=torch.int64)
+    registry = registry.to(device)
     seq = torch.tensor([kept + 1], dtype=torch.int64, device=device)
     indptr = torch.empty(2, dtype=torch.int32, device=device)
     kv = torch.empty(kept + 1, dtype=torch.int32, device=device)
@@ -47,7 +44,7 @@ def test_graph_replays_match_eager(device):
         ops.reposition_kv_layers(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], out.copy_src, out.copy_dst,
                                  out.copy_pairs, rope)
         page_table.build_indptr(seq, indptr)
-        registry.fill(rows, seq, indptr, kv)
+        page_table.context_decode_indices(registry, table, rows, seq, indptr, kv)
 
     dst = fresh.long()
     step()
@@ -87,7 +84,6 @@ def test_graph_replays_attention_consumers(device):
     """Decode attention (with its workspace) and the prefill attention over
     fixed metadata captured in one graph: replays equal the eager outputs."""
     from akv_amd import attention
-    from akv_amd import context_attention as ca
 
     g = torch.Generator(device=device).manual_seed(21)
     hq, hkv, d = 64, 8, 64
@@ -103,9 +99,10 @@ def test_graph_replays_attention_consumers(device):
     o_dec = torch.empty_like(q)
     ws = torch.empty(attention.workspace_bytes(len(lengths), hkv, d, max(lengths)) // 4 + 1, dtype=torch.float32,
                      device=device)
-    plan = ca.ContextAttentionPlan.merge([ca.ContextSequence.ordinary(500, 77), ca.ContextSequence.ordinary(0, 30)])
-    occ = torch.from_numpy(rng.permutation(np.arange(1, slots))[: plan.occurrence_count].astype(np.int64)).to(device)
-    meta = plan.bind(occ)
+    requests = [plain_segments(500, 77), plain_segments(0, 30)]
+    occ = torch.from_numpy(rng.permutation(np.arange(1, slots))[: sum(r.occurrences for r in requests)]
+                           .astype(np.int64)).to(device)
+    meta = attention_metadata(requests, occ)
     nq = meta.query_count
     qe = torch.randn((nq, hq, d), generator=g, device=device).to(torch.bfloat16)
     ke = torch.randn((nq, hkv, d), generator=g, device=device).to(torch.bfloat16)
@@ -116,8 +113,7 @@ def test_graph_replays_attention_consumers(device):
     def step():
         attention.decode_attention(q, k, v, indptr, idx, o_dec, scale=0.125, max_len=max(lengths), sinks=sinks,
                                    workspace=ws)
-        meta.forward(ca.extend_attention_fwd, qe, ke, ve, o_pre, k, v, sm_scale=0.125, sliding_window_size=64,
-                     sinks=sinks)
+        prefill_forward(meta, qe, ke, ve, o_pre, k, v, sm_scale=0.125, sliding_window_size=64, sinks=sinks)
 
     step()
     torch.cuda.synchronize()

@@ -9,7 +9,7 @@ import torch
 
 import ownership_scenarios as scenarios
 from akv_amd import ownership
-from golden import make_ownership_vectors as vectors
+from golden import ownership_vectors as vectors
 
 pytestmark = pytest.mark.gpu
 

@@ -23,7 +23,7 @@ import numpy as np
 import pytest
 
 import ownership_scenarios as scenarios
-from golden import make_ownership_vectors as vectors
+from golden import ownership_vectors as vectors
 from oracle import events as ev
 from oracle import occurrence as occ
 from oracle import ownership as own

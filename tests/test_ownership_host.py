@@ -14,7 +14,7 @@ import torch
 
 import ownership_scenarios as scenarios
 from akv_amd import ownership
-from golden import make_ownership_vectors as vectors
+from golden import ownership_vectors as vectors
 
 
 def _gather_on_cpu(self, extra_i32=()):
