@@ -7,13 +7,19 @@ A drop-in for the KV-cache hot path of thu-nics/AKV:
 * ``akv_amd.tables.compact_rows`` -- batched page-table compaction: terminal
   request rows, freed slots, copy lists, decode layout and compacted rows;
 * ``akv_amd.page_table`` -- decode indices, window lengths, indptr rebuild
-  and side-row scatter over the reference registry's rows;
+  over the reference registry's rows, and the side-row / extend writes of
+  request rows;
 * ``akv_amd.context_attention.extend_attention_fwd`` -- prefill attention
   over the compacted rows with context positions;
-* ``akv_amd.plan.compile_context_layout`` -- the host event compiler.
+* ``akv_amd.plan.compile_context_layout`` -- the host event compiler;
+* ``akv_amd.occurrence`` / ``akv_amd.ownership`` -- the prefill's occurrence
+  window and slot ownership across forwards;
+* ``akv_amd.transfer.copy_kv_rows`` -- K/V row copies of the P -> D handoff.
 
-The reference's own host classes (model binding, decode registry, prefill
-metadata, P -> D transfer planning) call these entry points unchanged.
+The reference's host classes (model binding, decode registry, prefill
+metadata, P -> D transfer planning, the request row store) stay the callers:
+each calls these functions where it called a Triton kernel or a numpy
+planner, with the same arguments.
 
 All device work is in ``libakv_amd.so`` (C ABI: ``include/akv_amd.h``),
 built by ``python -m akv_amd.build``.  There is no CPU fallback.

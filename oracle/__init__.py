@@ -15,6 +15,9 @@ reference repository root):
 ``reposition``  ``_reposition_layers_kernel`` op order
                 (``akv/system/sglang/kernels/ops/attention/context_reposition.py:54-123``)
                 and the wrapper's validation (``:126-236``).
+``cpu_torch``   the same Reposition arithmetic as torch CPU tensor operations
+                over every host thread: the CPU baseline that ``bench.py``
+                times, pinned bit for bit to ``reposition``.
 ``events``      the linked-list Drop/Reposition replay of
                 ``akv/system/sglang/kernels/ops/attention/context_plan.py:80-532``
                 and its driver ``akv/system/sglang/srt/context_system/ir.py:113-274``.
