@@ -30,6 +30,8 @@
 // wait for every load in flight, which serialises the tile.  Batches of up
 // to 512 requests keep their offsets, generated counts and rows in LDS
 // (STAGED); larger ones read them from memory.
+#include <atomic>
+
 #include "common.h"
 
 // Wavefront reduce / scan of the device library (DPP and lane reads, no
@@ -91,6 +93,11 @@ struct CompactArgs {
   int32_t* counts;
   int32_t* status;
   int4* tile_agg;      // [tiles] per-tile aggregates (kept, moved, retired, generated)
+  uint32_t* tile_pack; // [tiles] one-launch path: kept | moved << 16 of each tile
+  int2* tile_pre;      // [tiles + 1] one-launch path: kept, moved before each tile
+  int2* req_local;     // [B] one-launch path: kept, moved of a request's first tile before it
+  uint32_t* sync;      // one-launch path: barrier words, zero at rest
+  int32_t groups;      // one-launch path: arrival groups
   int64_t* req_gen;    // [B + 1] generated prefix: of every request (staged batches, count
                        // launch), of the tile's requests (others, tiles with more
                        // requests than the window)
@@ -106,6 +113,13 @@ __device__ __forceinline__ int lane_id() { return __lane_id(); }
 __device__ __forceinline__ int rank_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+}
+
+// A wave-uniform 64-bit value moved to scalar registers.
+__device__ __forceinline__ int64_t uniform(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint64_t>(v)));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 __device__ __forceinline__ int32_t* row_base(const CompactArgs& a, int64_t b) {
@@ -433,14 +447,332 @@ __device__ __forceinline__ void emit_token(const CompactArgs& a, bool kept, int3
   row[local] = terminal;
 }
 
-// Per tile: the exclusive prefix, then every output the tile owns.
+// Element i of a flat output through a 32-bit byte offset from the array
+// base (i < 2^29), so the store takes a scalar base and one offset register.
+__device__ __forceinline__ void put32(int32_t* base, uint32_t i, int32_t v) {
+  *reinterpret_cast<int32_t*>(reinterpret_cast<char*>(base) + (i << 2)) = v;
+}
+
+// emit_token for batches whose positions and output sizes stay below 2^29.
+__device__ __forceinline__ void emit_token32(const CompactArgs& a, bool kept, int32_t bpos, int32_t fpos,
+                                             int32_t slot, int32_t fresh, uint32_t pk, uint32_t pm, uint32_t pr,
+                                             int32_t* row, int32_t local, uint32_t shift) {
+  const bool moved = kept && bpos != fpos;
+  const bool retired = !kept || moved;
+  int32_t terminal = -1;
+  if (moved) {
+    terminal = fresh;
+    if (pm < a.fresh_count) {
+      put32(a.copy_src, pm, slot);
+      put32(a.copy_dst, pm, fresh);
+      put32(a.copy_pairs, 2 * pm, bpos);
+      put32(a.copy_pairs, 2 * pm + 1, fpos);
+    }
+  } else if (kept) {
+    terminal = slot;
+  }
+  if (retired && pr < a.retired_capacity) put32(a.retired, pr, slot);
+  if (kept && pk < a.kept_capacity) {
+    put32(a.raw_indices, pk, local);
+    put32(a.active_positions, pk, fpos);
+  }
+  if (kept && a.kv_indices && pk + shift < a.kv_capacity) put32(a.kv_indices, pk + shift, terminal);
+  row[local] = terminal;
+}
+
+// The tile's requests, from counts of offsets <= x over off[0, B] (found by
+// tile_masks):
+//   owned  [own_lo, own_hi): start in [t0, t1), the last tile also at t1
+//   tokens [w0, tok_hi):     hold the tile's tokens (w0 = own_lo - 1)
+//   closed [close_lo - 1, close_hi - 1): end in (t0, t1], tile 0 also at 0
+struct TileRequests {
+  int64_t own_lo, own_hi, tok_hi, close_lo, close_hi, w0;
+  int count;      // requests holding the tile's tokens, or -1 past kWindow
+  bool spans_in;  // request w0 starts in an earlier tile and ends in this one
+};
+
+template <int STEPS, bool STAGED>
+__device__ __forceinline__ TileRequests tile_requests(const CompactArgs& a, const Tile<STEPS, STAGED>& sh,
+                                                      int64_t tile) {
+  TileRequests r;
+  r.own_lo = uniform(sh.s_count[0]);
+  r.tok_hi = uniform(sh.s_count[1]);
+  r.own_hi = tile == a.tiles - 1 ? static_cast<int64_t>(a.n_requests) + 1 : r.tok_hi;
+  r.close_lo = tile == 0 ? 1 : uniform(sh.s_count[2]);
+  r.close_hi = uniform(sh.s_count[3]);
+  r.w0 = r.own_lo > 0 ? r.own_lo - 1 : 0;
+  r.count = r.tok_hi - r.w0 <= kWindow ? static_cast<int>(r.tok_hi - r.w0) : -1;
+  r.spans_in = r.own_lo > 0 && r.close_lo - 1 == r.w0 && r.close_lo < r.close_hi;
+  return r;
+}
+
+// Offsets, generated prefixes and raw rows of the requests holding the
+// tile's tokens, in LDS.
+struct Window {
+  int64_t off[kWindow + 1];
+  int64_t gen[kWindow];
+  int32_t* row[kWindow];
+};
+
+template <int STEPS, bool STAGED>
+__device__ __forceinline__ void fill_window(const Requests<STEPS, STAGED>& rq, const TileRequests& r, Window& win) {
+  if (r.count >= 0)
+    for (int k = threadIdx.x; k <= r.count; k += kThreads) {
+      const int64_t b = r.w0 + k;
+      win.off[k] = rq.off(b);
+      if (k < r.count) win.row[k] = rq.row(b);
+    }
+}
+
+// Every output of the tile, from its exclusive prefix `sums` and, when
+// spans_in, the start counts of request w0.  With write_status the last
+// tile also writes the status word.  A token's kept flag comes from the
+// tile's ballots, and its rank among retired tokens from the identity
+// retired-before = tokens-before - kept-before + moved-before.  SMALL
+// batches (positions and output sizes below 2^29) keep token positions and
+// ranks in 32 bits.
+template <int STEPS, bool STAGED, bool SMALL>
+__device__ __forceinline__ void tile_outputs(const CompactArgs& a, Tile<STEPS, STAGED>& sh, Window& win,
+                                             const TileRequests& r, int64_t tile, int64_t t0, int64_t t1,
+                                             const int64_t (&sums)[kCounters], const int64_t (&span_start)[3],
+                                             const int32_t (&bps)[STEPS], const int32_t (&fps)[STEPS],
+                                             const int32_t (&slot0)[STEPS], bool write_status) {
+  using T = Tile<STEPS, STAGED>;
+  const int w = threadIdx.x >> 6;
+  const TileMasks<T::kBlks>& m = sh.m;
+  const Requests<STEPS, STAGED> rq{a, sh};
+  // requests that start in the tile: kv_indptr, the generated tail of the
+  // request before
+  int64_t gen_total;
+  if constexpr (STAGED) {
+    gen_total = sh.s_genx[a.n_requests];
+    for (int64_t b = r.own_lo + threadIdx.x; b < r.own_hi; b += kThreads) {
+      const int64_t ob = rq.off(b);
+      const int64_t at = sums[0] + m.count_before(ob - t0, 0) + sh.s_genx[b];  // kv_indptr[b]
+      if (a.kv_indptr) a.kv_indptr[b] = static_cast<int32_t>(at);
+      const int64_t g = b > 0 ? rq.gen(b - 1) : 0;
+      if (g > 0 && a.kv_indices) {
+        const int32_t* row = rq.row(b - 1);
+        const int64_t n = ob - rq.off(b - 1);
+        for (int64_t i = 0; i < g; ++i)
+          if (at - g + i >= 0 && at - g + i < a.kv_capacity) a.kv_indices[at - g + i] = row[n + i];
+      }
+    }
+  } else {
+    int64_t carry = sums[3];
+    for (int64_t base = r.own_lo; base < r.own_hi; base += kThreads) {
+      const int64_t b = base + threadIdx.x;
+      const bool mine = b < r.own_hi;
+      int64_t pre, sum;
+      block_scan(mine ? rq.gen(b) : 0, sh.lds, pre, sum);
+      if (mine) {
+        const int64_t gen_b = carry + pre;
+        const int64_t ob = rq.off(b);
+        const int64_t at = sums[0] + m.count_before(ob - t0, 0) + gen_b;  // kv_indptr[b]
+        if (a.kv_indptr) a.kv_indptr[b] = static_cast<int32_t>(at);
+        const int64_t g = b > 0 ? rq.gen(b - 1) : 0;
+        if (g > 0 && a.kv_indices) {
+          const int32_t* row = rq.row(b - 1);
+          const int64_t n = ob - rq.off(b - 1);
+          for (int64_t i = 0; i < g; ++i)
+            if (at - g + i >= 0 && at - g + i < a.kv_capacity) a.kv_indices[at - g + i] = row[n + i];
+        }
+        if (r.count >= 0) {
+          if (b - r.w0 < r.count) win.gen[b - r.w0] = gen_b;
+        } else {
+          __hip_atomic_store(a.req_gen + b, gen_b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      carry += sum;
+    }
+    if (r.count >= 0 && r.own_lo > 0 && threadIdx.x == 0) win.gen[0] = sums[3] - rq.gen(r.w0);
+    gen_total = carry;  // the last tile's carry: every generated entry
+  }
+  if (write_status && tile == a.tiles - 1 && threadIdx.x == 0 && a.status) {
+    const int64_t kept = sums[0] + m.before[T::kBlks][0];
+    const int64_t moved = sums[1] + m.before[T::kBlks][1];
+    const int64_t retired = sums[2] + m.before[T::kBlks][2];
+    const bool bad = moved != a.fresh_count || kept > a.kept_capacity || retired > a.retired_capacity ||
+                     (a.kv_indices && kept + gen_total > a.kv_capacity);
+    a.status[0] = bad ? 1 : 0;
+  }
+
+  // requests that end in the tile: counts and last-page lengths
+  for (int64_t i = r.close_lo + threadIdx.x; i < r.close_hi; i += kThreads) {
+    const int64_t b = i - 1;
+    const int64_t lo = rq.off(b), hi = rq.off(i);
+    int64_t start[3], end[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      end[c] = sums[c] + m.count_before(hi - t0, c);
+      start[c] = lo >= t0 ? sums[c] + m.count_before(lo - t0, c) : span_start[c];  // lo < t0: b == w0
+    }
+    const int64_t kept = end[0] - start[0];
+    if (a.counts) {
+      a.counts[3 * b] = static_cast<int32_t>(kept);
+      a.counts[3 * b + 1] = static_cast<int32_t>(end[1] - start[1]);
+      a.counts[3 * b + 2] = static_cast<int32_t>(end[2] - start[2]);
+    }
+    if (a.last_page_len) {
+      const int64_t len = kept + rq.gen(b);
+      a.last_page_len[b] = len > 0 ? static_cast<int32_t>((len - 1) % a.page_size + 1) : 0;
+    }
+  }
+  if (r.count < 0) {
+    // the generated prefixes above are read back by other threads below
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
+  }
+  __syncthreads();
+  if (t1 <= t0) return;
+
+  // Per-token outputs: every load first (birth slots from the raw rows,
+  // fresh slots), then one wait, then the stores, so no store waits behind
+  // another.  Lanes past t1 load for token t1 - 1 and store nothing.
+  const int64_t fresh_last = a.fresh_count > 0 ? a.fresh_count - 1 : 0;
+  if (SMALL && r.count >= 0) {
+    const int32_t k0 = static_cast<int32_t>(sums[0]), m0 = static_cast<int32_t>(sums[1]);
+    const int32_t u0 = static_cast<int32_t>(t0), u1 = static_cast<int32_t>(t1);
+    const int32_t flast = static_cast<int32_t>(fresh_last);
+    // the request holding token tc (a search of the window)
+    auto find = [&](int32_t tc) {
+      int l = 0, h = r.count - 1;  // off[l] <= tc < off[h + 1]
+      while (l < h) {
+        const int mid = (l + h + 1) >> 1;
+        if (static_cast<int32_t>(win.off[mid]) <= tc)
+          l = mid;
+        else
+          h = mid - 1;
+      }
+      return l;
+    };
+    int32_t slots[STEPS], fr[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int32_t t = u0 + s * kThreads + static_cast<int32_t>(threadIdx.x);
+      const int32_t tc = t < u1 ? t : u1 - 1;
+      if (a.birth_slots) {
+        slots[s] = slot0[s];
+      } else {
+        const int l = find(tc);
+        slots[s] = win.row[l][tc - static_cast<int32_t>(win.off[l])];
+      }
+      const int p = s * kWaves + w;
+      const int32_t pm = m0 + m.before[p][1] + rank_below(m.bits[p][1]);
+      const int32_t f = a.fresh[pm < flast ? pm : flast];
+      fr[s] = pm < a.fresh_count ? f : -1;
+    }
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
+    asm volatile("" ::: "memory");  // the searches below are redone, not kept in registers
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int32_t t = u0 + s * kThreads + static_cast<int32_t>(threadIdx.x);
+      if (t >= u1) continue;
+      const int p = s * kWaves + w;
+      const int l = find(t);
+      const uint64_t kbits = m.bits[p][0];
+      const int32_t pk = k0 + m.before[p][0] + rank_below(kbits);
+      const int32_t pm = m0 + m.before[p][1] + rank_below(m.bits[p][1]);
+      emit_token32(a, (kbits >> lane_id()) & 1, bps[s], fps[s], slots[s], fr[s], pk, pm, t - pk + pm, win.row[l],
+                   t - static_cast<int32_t>(win.off[l]), static_cast<uint32_t>(sh.s_genx[r.w0 + l]));
+    }
+  } else if (r.count >= 0) {
+    int32_t req[STEPS], slots[STEPS], fr[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int64_t t = t0 + s * kThreads + threadIdx.x;
+      const int64_t tc = t < t1 ? t : t1 - 1;
+      int l = 0, h = r.count - 1;  // off[l] <= tc < off[h + 1]
+      while (l < h) {
+        const int mid = (l + h + 1) >> 1;
+        if (win.off[mid] <= tc)
+          l = mid;
+        else
+          h = mid - 1;
+      }
+      req[s] = l;
+      // the birth slot: from the flat vector (already loaded), else the raw row
+      slots[s] = a.birth_slots ? slot0[s] : win.row[l][tc - win.off[l]];
+      const int p = s * kWaves + w;
+      const int64_t pm = sums[1] + m.before[p][1] + rank_below(m.bits[p][1]);
+      const int32_t f = a.fresh[pm < fresh_last ? pm : fresh_last];
+      fr[s] = pm < a.fresh_count ? f : -1;
+    }
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int64_t t = t0 + s * kThreads + threadIdx.x;
+      if (t >= t1) continue;
+      const int p = s * kWaves + w;
+      const int l = req[s];
+      int64_t shift;
+      if constexpr (STAGED)
+        shift = sh.s_genx[r.w0 + l];
+      else
+        shift = win.gen[l];
+      const uint64_t kbits = m.bits[p][0];
+      const int64_t pk = sums[0] + m.before[p][0] + rank_below(kbits);
+      const int64_t pm = sums[1] + m.before[p][1] + rank_below(m.bits[p][1]);
+      emit_token(a, (kbits >> lane_id()) & 1, bps[s], fps[s], slots[s], fr[s], pk, pm, t - pk + pm, win.row[l],
+                 t - win.off[l], shift);
+    }
+  } else {
+    // more requests than the window: look each token's request up
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int64_t t = t0 + s * kThreads + threadIdx.x;
+      if (t >= t1) continue;
+      int64_t l = r.w0, h = r.tok_hi - 1;
+      while (l < h) {
+        const int64_t mid = (l + h + 1) >> 1;
+        if (rq.off(mid) <= t)
+          l = mid;
+        else
+          h = mid - 1;
+      }
+      int32_t* row = rq.row(l);
+      const int64_t local = t - rq.off(l);
+      int64_t shift;
+      if constexpr (STAGED)
+        shift = sh.s_genx[l];
+      else
+        shift = l >= r.own_lo ? __hip_atomic_load(a.req_gen + l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : sums[3] - rq.gen(l);
+      const int p = s * kWaves + w;
+      const uint64_t kbits = m.bits[p][0];
+      const bool kept = (kbits >> lane_id()) & 1;
+      const int64_t pk = sums[0] + m.before[p][0] + rank_below(kbits);
+      const int64_t pm = sums[1] + m.before[p][1] + rank_below(m.bits[p][1]);
+      const bool moved = kept && bps[s] != fps[s];
+      const int32_t slot = a.birth_slots ? slot0[s] : row[local];
+      const int32_t fresh = (moved && pm < a.fresh_count) ? a.fresh[pm] : -1;
+      emit_token(a, kept, bps[s], fps[s], slot, fresh, pk, pm, t - pk + pm, row, local, shift);
+    }
+  }
+}
+
+// Birth slots from the flat vector, in the same round as the other inputs.
+template <int STEPS>
+__device__ __forceinline__ void load_birth_slots(const CompactArgs& a, int64_t t0, int64_t t1,
+                                                 int32_t (&slot0)[STEPS]) {
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) slot0[s] = 0;
+  if (!a.birth_slots || t1 <= t0) return;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int64_t t = t0 + s * kThreads + threadIdx.x;
+    slot0[s] = a.birth_slots[t < t1 ? t : t1 - 1];
+  }
+}
+
+// Two-launch path, second launch: per tile, the exclusive prefix summed from
+// every earlier tile's aggregate, then every output the tile owns.
 template <int STEPS, bool STAGED>
 __global__ void __launch_bounds__(kThreads) scatter_kernel(const CompactArgs a) {
   using T = Tile<STEPS, STAGED>;
   __shared__ T sh;
-  const int w = threadIdx.x >> 6;
+  __shared__ Window win;
   const int64_t tile = blockIdx.x;
-  const bool last_tile = tile == a.tiles - 1;
   const int64_t t0 = tile * T::kTile;
   const int64_t t1 = t0 + T::kTile < a.total ? t0 + T::kTile : a.total;
   // aggregates of earlier tiles: the first batch in flight with the inputs
@@ -451,8 +783,9 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(const CompactArgs a) 
     agg[u] = a.tile_agg[i < tile ? i : 0];
   }
   uint8_t kb[STEPS];
-  int32_t bps[STEPS], fps[STEPS];
+  int32_t bps[STEPS], fps[STEPS], slot0[STEPS];
   load_inputs<STEPS>(a, t0, t1, kb, bps, fps);
+  load_birth_slots<STEPS>(a, t0, t1, slot0);
   stage_requests<STEPS, STAGED>(a, sh);
   // this thread's share of the exclusive prefix: kept, moved, retired and
   // (batches that are not staged) generated entries before the tile
@@ -473,34 +806,11 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(const CompactArgs a) 
       agg[u] = a.tile_agg[i < tile ? i : 0];
     }
   }
-  // The tile's requests, from counts of offsets <= x over off[0, B]:
-  //   owned  [own_lo, own_hi): start in [t0, t1), the last tile also at t1
-  //   tokens [w0, tok_hi):     hold the tile's tokens (w0 = own_lo - 1)
-  //   closed [close_lo - 1, close_hi - 1): end in (t0, t1], tile 0 also at 0
   const int64_t x[kWaves] = {t0 - 1, t1 - 1, t0, t1};
   tile_masks<STEPS, STAGED>(a, sh, t0, t1, x, kb, bps, fps);
-  const TileMasks<T::kBlks>& m = sh.m;
+  const TileRequests r = tile_requests<STEPS, STAGED>(a, sh, tile);
   const Requests<STEPS, STAGED> rq{a, sh};
-  const int64_t n_off = static_cast<int64_t>(a.n_requests) + 1;
-  const int64_t own_lo = sh.s_count[0];
-  const int64_t tok_hi = sh.s_count[1];
-  const int64_t own_hi = last_tile ? n_off : tok_hi;
-  const int64_t close_lo = tile == 0 ? 1 : sh.s_count[2];
-  const int64_t close_hi = sh.s_count[3];
-  const int64_t w0 = own_lo > 0 ? own_lo - 1 : 0;
-  const int count = tok_hi - w0 <= kWindow ? static_cast<int>(tok_hi - w0) : -1;
-  // request w0 starts in an earlier tile j0 and ends in this one
-  const bool spans_in = own_lo > 0 && close_lo - 1 == w0 && close_lo < close_hi;
-
-  __shared__ int64_t woff[kWindow + 1];
-  __shared__ int64_t wgen[kWindow];
-  __shared__ int32_t* wrow[kWindow];
-  if (count >= 0)
-    for (int k = threadIdx.x; k <= count; k += kThreads) {
-      const int64_t b = w0 + k;
-      woff[k] = rq.off(b);
-      if (k < count) wrow[k] = rq.row(b);
-    }
+  fill_window<STEPS, STAGED>(rq, r, win);
   __shared__ int64_t red[kWaves][kCounters];
   block_sums<kCounters>(sums, red);
   // sums: kept, moved, retired (and generated, not staged) before the tile
@@ -509,8 +819,8 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(const CompactArgs a) 
   // of tile j0 from the request's first one, i.e. this tile's prefix minus
   // the aggregates of tiles (j0, tile) minus a recount of that stretch.
   __shared__ int64_t span_start[3];
-  if (spans_in) {
-    const int64_t lo = rq.off(w0);
+  if (r.spans_in) {
+    const int64_t lo = rq.off(r.w0);
     const int64_t j0 = lo / T::kTile;
     const int64_t hi = (j0 + 1) * T::kTile;  // < t0 <= total
     int64_t v[3] = {0, 0, 0};
@@ -538,176 +848,286 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(const CompactArgs a) 
     if (threadIdx.x == 0)
 #pragma unroll
       for (int c = 0; c < 3; ++c) span_start[c] = sums[c] - v[c];
+    __syncthreads();
   }
-
-  // requests that start in the tile: kv_indptr, the generated tail of the
-  // request before
-  int64_t gen_total;
-  if constexpr (STAGED) {
-    gen_total = sh.s_genx[a.n_requests];
-    for (int64_t b = own_lo + threadIdx.x; b < own_hi; b += kThreads) {
-      const int64_t ob = rq.off(b);
-      const int64_t at = sums[0] + m.count_before(ob - t0, 0) + sh.s_genx[b];  // kv_indptr[b]
-      if (a.kv_indptr) a.kv_indptr[b] = static_cast<int32_t>(at);
-      const int64_t g = b > 0 ? rq.gen(b - 1) : 0;
-      if (g > 0 && a.kv_indices) {
-        const int32_t* row = rq.row(b - 1);
-        const int64_t n = ob - rq.off(b - 1);
-        for (int64_t i = 0; i < g; ++i)
-          if (at - g + i >= 0 && at - g + i < a.kv_capacity) a.kv_indices[at - g + i] = row[n + i];
-      }
-    }
-  } else {
-    int64_t carry = sums[3];
-    for (int64_t base = own_lo; base < own_hi; base += kThreads) {
-      const int64_t b = base + threadIdx.x;
-      const bool mine = b < own_hi;
-      int64_t pre, sum;
-      block_scan(mine ? rq.gen(b) : 0, sh.lds, pre, sum);
-      if (mine) {
-        const int64_t gen_b = carry + pre;
-        const int64_t ob = rq.off(b);
-        const int64_t at = sums[0] + m.count_before(ob - t0, 0) + gen_b;  // kv_indptr[b]
-        if (a.kv_indptr) a.kv_indptr[b] = static_cast<int32_t>(at);
-        const int64_t g = b > 0 ? rq.gen(b - 1) : 0;
-        if (g > 0 && a.kv_indices) {
-          const int32_t* row = rq.row(b - 1);
-          const int64_t n = ob - rq.off(b - 1);
-          for (int64_t i = 0; i < g; ++i)
-            if (at - g + i >= 0 && at - g + i < a.kv_capacity) a.kv_indices[at - g + i] = row[n + i];
-        }
-        if (count >= 0) {
-          if (b - w0 < count) wgen[b - w0] = gen_b;
-        } else {
-          __hip_atomic_store(a.req_gen + b, gen_b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-      carry += sum;
-    }
-    if (count >= 0 && own_lo > 0 && threadIdx.x == 0) wgen[0] = sums[3] - rq.gen(w0);
-    gen_total = carry;  // the last tile's carry: every generated entry
-  }
-  if (last_tile && threadIdx.x == 0 && a.status) {
-    const int64_t kept = sums[0] + m.before[T::kBlks][0];
-    const int64_t moved = sums[1] + m.before[T::kBlks][1];
-    const int64_t retired = sums[2] + m.before[T::kBlks][2];
-    const bool bad = moved != a.fresh_count || kept > a.kept_capacity || retired > a.retired_capacity ||
-                     (a.kv_indices && kept + gen_total > a.kv_capacity);
-    a.status[0] = bad ? 1 : 0;
-  }
-  if (spans_in) __syncthreads();  // span_start
-
-  // requests that end in the tile: counts and last-page lengths
-  for (int64_t i = close_lo + threadIdx.x; i < close_hi; i += kThreads) {
-    const int64_t b = i - 1;
-    const int64_t lo = rq.off(b), hi = rq.off(i);
-    int64_t start[3], end[3];
+  int64_t start_w0[3];
 #pragma unroll
-    for (int c = 0; c < 3; ++c) {
-      end[c] = sums[c] + m.count_before(hi - t0, c);
-      start[c] = lo >= t0 ? sums[c] + m.count_before(lo - t0, c) : span_start[c];  // lo < t0: b == w0
+  for (int c = 0; c < 3; ++c) start_w0[c] = r.spans_in ? span_start[c] : 0;
+  tile_outputs<STEPS, STAGED, false>(a, sh, win, r, tile, t0, t1, sums, start_w0, bps, fps, slot0, true);
+}
+
+// ---- One-launch path: every tile resident at once ------------------------
+//
+// A tile loads its inputs once, publishes its kept and moved counts (and,
+// for the requests that start in it, their counts before their first token;
+// retired counts follow from tokens - kept + moved), and arrives at
+// a barrier.  The last tile to arrive scans every tile's counts into the
+// exclusive prefixes and releases the others; each tile then writes its
+// outputs.  Arrivals are counted per group of tiles (tile mod groups), the
+// last of a group arriving at one top counter, so no address takes more than
+// about tiles / groups atomics; each group polls its own generation word.
+// Every counter is zero at rest: the last arrival of a group or at the top
+// resets it, so the workspace must be zero before its first use.  What
+// crosses tiles (counts, prefixes, barrier words, the status word) moves by
+// agent-scope atomic loads and stores, ordered by waiting for completion;
+// no cache-wide fence is needed.  Waits are
+// bounded: a tile that stops waiting cancels its group's generation word by
+// compare-and-swap, so a release and a withdrawal exclude each other, skips
+// its outputs, and the status word reads 3.  Tile 0 sets the status word to
+// 2 first, which the last arrival overwrites.  All tiles of one launch fit
+// on the device at once (the host checks occupancy), so waits end in
+// practice long before the bound.
+
+constexpr int kGroups = 32;
+constexpr int kSyncStride = 32;  // one 128-byte line per word
+constexpr uint32_t kCancelled = 0x80000000u;
+constexpr uint32_t kPollLimit = 1u << 20;  // ~1 s of polling at most
+constexpr int kFusedScanPer = 8;
+constexpr int64_t kFusedMaxTiles = static_cast<int64_t>(kThreads) * kFusedScanPer;
+constexpr int64_t kSyncBytes = static_cast<int64_t>(2 * kGroups + 1) * kSyncStride * 4;
+
+// Data that one tile writes and another reads within the launch goes through
+// agent-scope atomic loads and stores, which the device keeps coherent across
+// its L2 slices without cache-wide write-back or invalidation; a writer waits
+// for its stores to complete (vmcnt) before it signals.
+__device__ __forceinline__ void put_pair(int2* p, int32_t x, int32_t y) {
+  const uint64_t v = static_cast<uint64_t>(static_cast<uint32_t>(x)) | (static_cast<uint64_t>(static_cast<uint32_t>(y)) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int2 get_pair(const int2* p) {
+  const uint64_t v =
+      __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_int2(static_cast<int32_t>(static_cast<uint32_t>(v)), static_cast<int32_t>(static_cast<uint32_t>(v >> 32)));
+}
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8)); }
+
+__device__ __forceinline__ uint32_t* arrive_word(const CompactArgs& a, int g) { return a.sync + g * kSyncStride; }
+__device__ __forceinline__ uint32_t* top_word(const CompactArgs& a) { return a.sync + kGroups * kSyncStride; }
+__device__ __forceinline__ uint32_t* gen_word(const CompactArgs& a, int g) {
+  return a.sync + (kGroups + 1 + g) * kSyncStride;
+}
+
+// Thread 0: polls the group's generation word read before arriving (g).
+// True once the last tile has released the group; false when this tile
+// withdrew (the wait ran out) or another tile of the group withdrew.
+__device__ bool wait_release(uint32_t* gen, uint32_t g) {
+  for (uint32_t polls = 0;; ++polls) {
+    const uint32_t v = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (v != g) return v != (g | kCancelled);
+    if (polls >= kPollLimit) {
+      uint32_t expected = g;
+      if (__hip_atomic_compare_exchange_strong(gen, &expected, g | kCancelled, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT))
+        return false;
+      return expected != (g | kCancelled);
     }
-    const int64_t kept = end[0] - start[0];
-    if (a.counts) {
-      a.counts[3 * b] = static_cast<int32_t>(kept);
-      a.counts[3 * b + 1] = static_cast<int32_t>(end[1] - start[1]);
-      a.counts[3 * b + 2] = static_cast<int32_t>(end[2] - start[2]);
-    }
-    if (a.last_page_len) {
-      const int64_t len = kept + rq.gen(b);
-      a.last_page_len[b] = len > 0 ? static_cast<int32_t>((len - 1) % a.page_size + 1) : 0;
-    }
+    __builtin_amdgcn_s_sleep(4);
   }
-  if (count < 0) {
-    // the generated prefixes above are read back by other threads below
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
+}
+
+// The last tile to arrive: exclusive (kept, moved) prefixes of every tile,
+// the status word, then the release of every group.  Each thread sums 8
+// consecutive tiles' packed counts (each half stays below 2^16).
+template <int STEPS>
+__device__ void scan_and_release(const CompactArgs& a, const Tile<STEPS, true>& sh) {
+  constexpr int K = kFusedScanPer;
+  const int w = threadIdx.x >> 6;
+  const int64_t first = static_cast<int64_t>(threadIdx.x) * K;
+  uint32_t v[K];
+#pragma unroll
+  for (int u = 0; u < K; ++u) {
+    const int64_t i = first + u;
+    v[u] = __hip_atomic_load(a.tile_pack + (i < a.tiles ? i : a.tiles - 1), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
+  uint32_t own = 0;
+#pragma unroll
+  for (int u = 0; u < K; ++u) own += first + u < a.tiles ? v[u] : 0u;
+  __shared__ int32_t part[kWaves][2];
+  int32_t pre[2], tot[2];
+  const int32_t mine[2] = {static_cast<int32_t>(own & 0xffffu), static_cast<int32_t>(own >> 16)};
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int32_t inc = __ockl_wfscan_add_i32(mine[c], true);
+    pre[c] = inc - mine[c];
+    if (lane_id() == 63) part[w][c] = inc;
   }
   __syncthreads();
-  if (t1 <= t0) return;
-
-  // Per-token outputs: every load first (birth slots, fresh slots), then
-  // one wait, then the stores, so no store waits behind another.  Lanes
-  // past t1 load for token t1 - 1 and store nothing.
-  const int64_t fresh_last = a.fresh_count > 0 ? a.fresh_count - 1 : 0;
-  if (count >= 0) {
-    int32_t req[STEPS], slots[STEPS], fr[STEPS];
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      const int64_t t = t0 + s * kThreads + threadIdx.x;
-      const int64_t tc = t < t1 ? t : t1 - 1;
-      int l = 0, h = count - 1;  // woff[l] <= tc < woff[h + 1]
-      while (l < h) {
-        const int mid = (l + h + 1) >> 1;
-        if (woff[mid] <= tc)
-          l = mid;
-        else
-          h = mid - 1;
-      }
-      req[s] = l;
-      // the birth slot: from the flat vector, else from the raw row
-      const int32_t* sp = a.birth_slots ? a.birth_slots + tc : wrow[l] + (tc - woff[l]);
-      slots[s] = *sp;
-      const int p = s * kWaves + w;
-      const int64_t pm = sums[1] + m.before[p][1] + rank_below(m.bits[p][1]);
-      const int32_t f = a.fresh[pm < fresh_last ? pm : fresh_last];
-      fr[s] = pm < a.fresh_count ? f : -1;
-    }
-    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      const int64_t t = t0 + s * kThreads + threadIdx.x;
-      if (t >= t1) continue;
-      const int p = s * kWaves + w;
-      const int l = req[s];
-      int64_t shift;
-      if constexpr (STAGED)
-        shift = sh.s_genx[w0 + l];
-      else
-        shift = wgen[l];
-      emit_token(a, kb[s] != 0, bps[s], fps[s], slots[s], fr[s], sums[0] + m.before[p][0] + rank_below(m.bits[p][0]),
-                 sums[1] + m.before[p][1] + rank_below(m.bits[p][1]),
-                 sums[2] + m.before[p][2] + rank_below(m.bits[p][2]), wrow[l], t - woff[l], shift);
-    }
-  } else {
-    // more requests than the window: look each token's request up
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      const int64_t t = t0 + s * kThreads + threadIdx.x;
-      if (t >= t1) continue;
-      int64_t l = w0, h = tok_hi - 1;
-      while (l < h) {
-        const int64_t mid = (l + h + 1) >> 1;
-        if (rq.off(mid) <= t)
-          l = mid;
-        else
-          h = mid - 1;
-      }
-      int32_t* row = rq.row(l);
-      const int64_t local = t - rq.off(l);
-      int64_t shift;
-      if constexpr (STAGED)
-        shift = sh.s_genx[l];
-      else
-        shift = l >= own_lo ? __hip_atomic_load(a.req_gen + l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                            : sums[3] - rq.gen(l);
-      const int p = s * kWaves + w;
-      const int64_t pm = sums[1] + m.before[p][1] + rank_below(m.bits[p][1]);
-      const bool moved = kb[s] != 0 && bps[s] != fps[s];
-      const int32_t slot = a.birth_slots ? a.birth_slots[t] : row[local];
-      const int32_t fresh = (moved && pm < a.fresh_count) ? a.fresh[pm] : -1;
-      emit_token(a, kb[s] != 0, bps[s], fps[s], slot, fresh, sums[0] + m.before[p][0] + rank_below(m.bits[p][0]), pm,
-                 sums[2] + m.before[p][2] + rank_below(m.bits[p][2]), row, local, shift);
+  for (int c = 0; c < 2; ++c) {
+    tot[c] = 0;
+    for (int q = 0; q < kWaves; ++q) {
+      if (q < w) pre[c] += part[q][c];
+      tot[c] += part[q][c];
     }
   }
+#pragma unroll
+  for (int u = 0; u < K; ++u) {
+    if (first + u < a.tiles) {
+      put_pair(a.tile_pre + first + u, pre[0], pre[1]);
+      pre[0] += static_cast<int32_t>(v[u] & 0xffffu);
+      pre[1] += static_cast<int32_t>(v[u] >> 16);
+    }
+  }
+  if (threadIdx.x == 0) put_pair(a.tile_pre + a.tiles, tot[0], tot[1]);
+  const int64_t retired = a.total - tot[0] + tot[1];
+  const bool bad = tot[1] != a.fresh_count || tot[0] > a.kept_capacity || retired > a.retired_capacity ||
+                   (a.kv_indices && tot[0] + sh.s_genx[a.n_requests] > a.kv_capacity);
+  wait_stores();
+  __syncthreads();
+  if (w == 0) {
+    // release every group: at most one withdrawal can change a word first
+    const int groups = a.groups;
+    bool cancelled = false;
+    if (lane_id() < groups) {
+      uint32_t* gen = gen_word(a, lane_id());
+      uint32_t g = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      cancelled = true;  // stays so only if every attempt fails, which no withdrawal can cause
+      for (int k = 0; k < 3; ++k) {
+        const uint32_t next = ((g & ~kCancelled) + 1u) & ~kCancelled;
+        uint32_t expected = g;
+        if (__hip_atomic_compare_exchange_strong(gen, &expected, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)) {
+          cancelled = (g & kCancelled) != 0;
+          break;
+        }
+        g = expected;
+      }
+    }
+    const bool any = __ballot(cancelled) != 0;
+    if (lane_id() == 0 && a.status)
+      __hip_atomic_store(a.status, any ? 3 : (bad ? 1 : 0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Scalar registers are capped at 88 (86 reported): measured on MI355X, a
+// 256-thread kernel holds 8 workgroups per CU up to 78 reported SGPRs, 7 up
+// to 94 and 6 from 98, while the occupancy query reports 8 up to 94; the
+// host applies the measured limit (kFusedMaxPerCu).
+template <int STEPS>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(88))) fused_kernel(const CompactArgs a) {
+  using T = Tile<STEPS, true>;
+  __shared__ T sh;
+  __shared__ Window win;
+  __shared__ uint32_t s_wait[2];  // [0]: 1 = last to arrive, 0 = wait; [1]: generation read before arriving
+  __shared__ uint32_t s_go;
+  const int64_t tile = blockIdx.x;
+  const int64_t t0 = tile * T::kTile;
+  const int64_t t1 = t0 + T::kTile < a.total ? t0 + T::kTile : a.total;
+  const int n = a.n_requests;
+  // status words are written by two tiles in order: coherent stores
+  if (tile == 0 && threadIdx.x == 0 && a.status)
+    __hip_atomic_store(a.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // one round of loads: the tile's inputs and flat birth slots, the batch's
+  // request offsets, rows and generated counts
+  uint8_t kb[STEPS];
+  int32_t bps[STEPS], fps[STEPS], slot0[STEPS];
+  load_inputs<STEPS>(a, t0, t1, kb, bps, fps);
+  load_birth_slots<STEPS>(a, t0, t1, slot0);
+  constexpr int kRounds = (kStagedRequests + kThreads) / kThreads;  // B + 1 offsets
+  int64_t gv[kRounds];
+#pragma unroll
+  for (int q = 0; q < kRounds; ++q) {
+    gv[q] = 0;
+    if (q * kThreads > n) break;
+    const int i = q * kThreads + threadIdx.x;
+    const int ic = i < n ? i : n - 1;
+    const int io = i <= n ? i : n;
+    const int64_t o = a.req_offsets[io];
+    const int64_t rr = a.req_rows[ic];
+    const int32_t g = a.generated ? a.generated[ic] : 0;
+    gv[q] = i < n ? g : 0;
+    if (i <= n) sh.s_off[i] = o;
+    if (i < n) sh.s_rr[i] = rr;
+  }
+  // exclusive prefix of generated entries over requests 0 .. B
+  int64_t gcarry = 0;
+#pragma unroll
+  for (int q = 0; q < kRounds; ++q) {
+    if (q * kThreads > n) break;
+    int64_t pre, sum;
+    block_scan(gv[q], sh.lds, pre, sum);
+    const int i = q * kThreads + threadIdx.x;
+    if (i <= n) sh.s_genx[i] = gcarry + pre;
+    gcarry += sum;
+  }
+  const int64_t x[kWaves] = {t0 - 1, t1 - 1, t0, t1};
+  tile_masks<STEPS, true>(a, sh, t0, t1, x, kb, bps, fps);
+  const TileRequests r = tile_requests<STEPS, true>(a, sh, tile);
+  const Requests<STEPS, true> rq{a, sh};
+  fill_window<STEPS, true>(rq, r, win);
+  // publish: the tile's counts, and the counts before each owned request
+  const TileMasks<T::kBlks>& m = sh.m;
+  for (int64_t b = r.own_lo + threadIdx.x; b < r.own_hi && b < n; b += kThreads) {
+    const int64_t q = rq.off(b) - t0;
+    put_pair(a.req_local + b, m.count_before(q, 0), m.count_before(q, 1));
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.tile_pack + tile,
+                       static_cast<uint32_t>(m.before[T::kBlks][0]) | (static_cast<uint32_t>(m.before[T::kBlks][1]) << 16),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  wait_stores();
+  __syncthreads();
+  const int groups = a.groups;
+  const int gi = static_cast<int>(tile % groups);
+  if (threadIdx.x == 0) {
+    // the generation is read (and the read complete) before arriving
+    const uint32_t g = __hip_atomic_load(gen_word(a, gi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_stores();
+    const uint32_t gsize = static_cast<uint32_t>((a.tiles - gi + groups - 1) / groups);
+    uint32_t last = 0;
+    if (__hip_atomic_fetch_add(arrive_word(a, gi), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gsize - 1) {
+      __hip_atomic_store(arrive_word(a, gi), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__hip_atomic_fetch_add(top_word(a), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+          static_cast<uint32_t>(groups) - 1) {
+        __hip_atomic_store(top_word(a), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = 1;
+      }
+    }
+    s_wait[0] = last;
+    s_wait[1] = g;
+  }
+  __syncthreads();
+  if (s_wait[0]) {
+    scan_and_release<STEPS>(a, sh);
+  } else {
+    if (threadIdx.x == 0) s_go = wait_release(gen_word(a, gi), s_wait[1]) ? 1u : 0u;
+    __syncthreads();
+    if (!s_go) return;
+  }
+  __syncthreads();
+  // the tile's prefix and, when a request spans in, its start counts
+  const int2 pre = get_pair(a.tile_pre + tile);
+  int64_t sums[kCounters];
+  sums[0] = __builtin_amdgcn_readfirstlane(pre.x);
+  sums[1] = __builtin_amdgcn_readfirstlane(pre.y);
+  sums[2] = t0 - sums[0] + sums[1];
+  sums[3] = 0;
+  int64_t start_w0[3] = {0, 0, 0};
+  if (r.spans_in) {
+    const int64_t lo = rq.off(r.w0);
+    const int2 pj = get_pair(a.tile_pre + lo / T::kTile);
+    const int2 loc = get_pair(a.req_local + r.w0);
+    start_w0[0] = __builtin_amdgcn_readfirstlane(pj.x + loc.x);
+    start_w0[1] = __builtin_amdgcn_readfirstlane(pj.y + loc.y);
+    start_w0[2] = lo - start_w0[0] + start_w0[1];
+  }
+  tile_outputs<STEPS, true, true>(a, sh, win, r, tile, t0, t1, sums, start_w0, bps, fps, slot0, false);
 }
 
 // Byte offsets of the workspace arrays (each 128-byte aligned).
 struct Layout {
-  int64_t tile_agg, req_gen, req_row, bytes;
+  int64_t sync, tile_agg, tile_prefix, req_local, req_gen, req_row, bytes;
 };
 
-Layout workspace_layout(int64_t n_requests, int64_t tiles) {
+// Sized for both paths: the barrier words first (at a fixed offset, so
+// batches of any size may share a workspace), then per-tile and
+// per-request arrays.
+Layout workspace_layout(int64_t n_requests, int64_t total) {
+  const int64_t two_launch = tile_count(total, tile_steps(total));
+  const int64_t per_step = (total + kThreads - 1) / kThreads;  // most tiles of the one-launch path
+  const int64_t one_launch = per_step < kFusedMaxTiles ? per_step : kFusedMaxTiles;
+  const int64_t tiles = two_launch > one_launch ? two_launch : one_launch;
   Layout l{};
   int64_t at = 0;
   auto take = [&at](int64_t bytes) {
@@ -715,11 +1135,63 @@ Layout workspace_layout(int64_t n_requests, int64_t tiles) {
     at += (bytes + 127) & ~static_cast<int64_t>(127);
     return here;
   };
+  l.sync = take(kSyncBytes);
   l.tile_agg = take(16 * tiles);
+  l.tile_prefix = take(8 * (tiles + 1));
+  l.req_local = take(8 * n_requests);
   l.req_gen = take(8 * (n_requests + 1));
   l.req_row = take(8 * n_requests);
   l.bytes = at;
   return l;
+}
+
+// One-launch tile sizes, in the order tried (the smallest that fits).
+constexpr int kFusedSteps[] = {1, 2, 3, 4, 5, 6, 8};
+constexpr int kFusedVariants = sizeof(kFusedSteps) / sizeof(kFusedSteps[0]);
+constexpr int kMaxDevices = 64;
+constexpr int kFusedMaxPerCu = 7;  // residency of fused_kernel's SGPR footprint (see its declaration)
+
+const void* fused_entry(int steps) {
+  switch (steps) {
+    case 1: return reinterpret_cast<const void*>(&fused_kernel<1>);
+    case 2: return reinterpret_cast<const void*>(&fused_kernel<2>);
+    case 3: return reinterpret_cast<const void*>(&fused_kernel<3>);
+    case 4: return reinterpret_cast<const void*>(&fused_kernel<4>);
+    case 5: return reinterpret_cast<const void*>(&fused_kernel<5>);
+    case 6: return reinterpret_cast<const void*>(&fused_kernel<6>);
+    default: return reinterpret_cast<const void*>(&fused_kernel<8>);
+  }
+}
+
+// Workgroups of fused_kernel<kFusedSteps[v]> resident at once on the current
+// device (0 when unknown), cached per device: the occupancy query (registers,
+// LDS) bounded by the measured SGPR limit.
+int64_t fused_capacity(int v) {
+  static std::atomic<int64_t> cache[kMaxDevices][kFusedVariants];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int64_t c = cache[dev][v].load(std::memory_order_relaxed);
+  if (c > 0) return c;
+  int blocks = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fused_entry(kFusedSteps[v]), kThreads, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  c = static_cast<int64_t>(blocks < kFusedMaxPerCu ? blocks : kFusedMaxPerCu) * cus;
+  cache[dev][v].store(c, std::memory_order_relaxed);
+  return c;
+}
+
+void launch_fused(int steps, const CompactArgs& a, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(a.tiles));
+  switch (steps) {
+    case 1: hipLaunchKernelGGL((fused_kernel<1>), grid, dim3(kThreads), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((fused_kernel<2>), grid, dim3(kThreads), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((fused_kernel<3>), grid, dim3(kThreads), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((fused_kernel<4>), grid, dim3(kThreads), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((fused_kernel<5>), grid, dim3(kThreads), 0, st, a); break;
+    case 6: hipLaunchKernelGGL((fused_kernel<6>), grid, dim3(kThreads), 0, st, a); break;
+    default: hipLaunchKernelGGL((fused_kernel<8>), grid, dim3(kThreads), 0, st, a); break;
+  }
 }
 
 template <int STEPS, bool STAGED>
@@ -743,7 +1215,7 @@ void launch(const CompactArgs& a, hipStream_t st) {
 extern "C" int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t total_tokens) {
   using namespace akv;
   if (n_requests < 0 || total_tokens < 0) return -1;
-  return workspace_layout(n_requests, tile_count(total_tokens, tile_steps(total_tokens))).bytes;
+  return workspace_layout(n_requests, total_tokens).bytes;
 }
 
 extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, int64_t total_tokens,
@@ -778,7 +1250,7 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
   const int64_t tiles = tile_count(total_tokens, steps);
   if (tiles > 0x7fffffffLL)
     return fail(AKV_EINVAL, "akv_compact_rows: %lld tokens exceed one launch", static_cast<long long>(total_tokens));
-  const Layout lay = workspace_layout(n_requests, tiles);
+  const Layout lay = workspace_layout(n_requests, total_tokens);
   if (workspace_bytes < lay.bytes)
     return fail(AKV_EINVAL, "akv_compact_rows: workspace holds %lld bytes, needs %lld",
                 static_cast<long long>(workspace_bytes), static_cast<long long>(lay.bytes));
@@ -814,7 +1286,11 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
   a.counts = counts;
   a.status = status;
   char* ws = static_cast<char*>(workspace);
+  a.sync = reinterpret_cast<uint32_t*>(ws + lay.sync);
   a.tile_agg = reinterpret_cast<int4*>(ws + lay.tile_agg);
+  a.tile_pack = reinterpret_cast<uint32_t*>(ws + lay.tile_agg);  // the paths never share a call
+  a.tile_pre = reinterpret_cast<int2*>(ws + lay.tile_prefix);
+  a.req_local = reinterpret_cast<int2*>(ws + lay.req_local);
   a.req_gen = reinterpret_cast<int64_t*>(ws + lay.req_gen);
   a.req_row = reinterpret_cast<int32_t**>(ws + lay.req_row);
   a.total = total_tokens;
@@ -822,6 +1298,19 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
   a.n_requests = n_requests;
 
   hipStream_t st = as_stream(stream);
+  constexpr int64_t kSmall = int64_t{1} << 29;  // 32-bit byte offsets of every output
+  if (n_requests <= kStagedRequests && total_tokens < kSmall && fresh_count < kSmall && retired_capacity < kSmall &&
+      kept_capacity < kSmall && (!kv_indices || kv_capacity < kSmall)) {
+    // one launch when a tile size exists whose tiles all fit on the device
+    for (int v = 0; v < kFusedVariants; ++v) {
+      const int64_t t = tile_count(total_tokens, kFusedSteps[v]);
+      if (t > kFusedMaxTiles || t > fused_capacity(v)) continue;
+      a.tiles = t;
+      a.groups = static_cast<int32_t>(t < kGroups ? t : kGroups);
+      launch_fused(kFusedSteps[v], a, st);
+      return check_launch("akv_compact_rows");
+    }
+  }
   switch (steps) {
     case 1:
       launch<1>(a, st);

@@ -141,7 +141,7 @@ def allocate_outputs(inputs, device, *, generated_total=None):
         last_page_len=None if indptr is None else torch.empty(inputs.n_requests, dtype=i32, device=device),
         counts=torch.empty((inputs.n_requests, 3), dtype=i32, device=device),
         status=torch.zeros(1, dtype=i32, device=device),
-        workspace=torch.empty(max(8, (ws_bytes + 7) // 8), dtype=torch.int64, device=device),
+        workspace=torch.zeros(max(8, (ws_bytes + 7) // 8), dtype=torch.int64, device=device),
     )
 
 
@@ -214,6 +214,23 @@ def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_po
             current_stream_handle(device),
         )
     _lib.check(rc, "akv_compact_rows")
+    return outputs
+
+
+_STATUS_TEXT = {
+    1: "fresh slot count or an output capacity does not match the batch",
+    2: "the one-launch barrier did not complete (workspace not zero-filled before its first use?)",
+    3: "a tile stopped waiting at the one-launch barrier (tiles could not all run at once)",
+}
+
+
+def check_status(outputs):
+    """Wait for the compaction and raise if its status word is not 0; its
+    outputs are then partial and must not reach the Reposition or the decode
+    metadata.  Synchronises with the device (one 4-byte read)."""
+    code = int(outputs.status.item())
+    if code:
+        raise RuntimeError(f"akv_compact_rows status {code}: {_STATUS_TEXT.get(code, 'unknown')}")
     return outputs
 
 

@@ -110,6 +110,7 @@ class Pipeline:
         kv_bytes = 2  # bf16
         self.retained_bytes = self.moved * 4 * m.n_layers * m.n_heads * m.head_dim * kv_bytes
         self.alg_bytes = self.retained_bytes + self.moved * 16 + self.moved * 2 * m.rotary_dim * 4
+        self.checked_compaction()
 
     def compaction(self):
         tables.compact_rows(self.inputs, self.table, self.rows, self.fresh, self.out, generated=self.generated,
@@ -123,6 +124,11 @@ class Pipeline:
     def step(self):
         self.compaction()
         self.reposition()
+
+    def checked_compaction(self):
+        # once, before any timed step: a failed compaction must not feed the Reposition
+        self.compaction()
+        tables.check_status(self.out)
 
     def flush(self):
         # read 1 GiB: evicts the MALL and L2 with clean lines, so the timed
@@ -244,6 +250,8 @@ def ragged_config(device, flush):
     def step():
         tables.compact_rows(inputs, table, rows, fresh, out, generated=gen, birth_slots=birth)
 
+    step()
+    tables.check_status(out)
     warm, cold = _time_steps(step, 50, 10, 50, flush)
     graph = _graph_steps(step, 50)
     total = sum(w.lengths)
@@ -283,6 +291,7 @@ def decode_consumer_config(device, flush):
     tables.compact_rows(inputs, table, rows, torch.from_numpy(np.concatenate(slots.fresh)).to(device), out,
                         generated=torch.ones(B, dtype=torch.int32, device=device),
                         birth_slots=torch.from_numpy(np.concatenate(slots.birth_rows)).to(device))
+    tables.check_status(out)
     pool = synth.make_pool(model, w.pool_slots, device, seed=9, generate_on_device=True)
 
     # registry rows (the reference registry's row format) straight from the

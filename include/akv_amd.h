@@ -71,9 +71,10 @@ int akv_reposition_kv_layers(const uint64_t* k_ptrs, const uint64_t* v_ptrs,
 
 /*
  * Device bytes of the workspace akv_compact_rows needs for a batch of
- * n_requests holding total_tokens raw tokens in all (16-byte aligned, no
- * clearing needed).  Calls that share a workspace must not overlap (issue
- * them on one stream).
+ * n_requests holding total_tokens raw tokens in all (16-byte aligned).  The
+ * workspace must be zero-filled once before its first use; every completed
+ * call leaves it ready for the next, whatever that call's batch size.  Calls
+ * that share a workspace must not overlap (issue them on one stream).
  */
 int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t total_tokens);
 
@@ -99,10 +100,19 @@ int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t total_tokens);
  *   last_page_len (opt.) [B] ((kept + generated - 1) % page_size) + 1, 0 if empty
  *   counts     (opt.)   [B,3] kept, moved, retired
  *   status     (opt.)   device int32: 0, or 1 if fresh_count or a capacity
- *                       does not match (outputs are then partial)
+ *                       does not match (outputs are then partial); 2 or 3
+ *                       if the one-launch path's bounded wait ran out (a
+ *                       workspace that was not zero-filled, or a device
+ *                       shared so heavily that the tiles could not all
+ *                       run at once; outputs are then partial)
  * retired, the copy lists and raw_indices / active_positions may be NULL
  * when retired_capacity, fresh_count and kept_capacity are 0.
- * Two launches: per-tile counts, then per-tile prefixes and every output.
+ * One launch when the batch has at most 512 requests, fewer than 2^29
+ * tokens (and list capacities) and some tile size lets every tile run on
+ * the device at once
+ * (tiles publish counts, the last to arrive scans them, all then write);
+ * otherwise two launches: per-tile counts, then per-tile prefixes and every
+ * output.
  * Replaces the CPU numpy/H2D path of OccurrenceState.advance +
  * terminal_slots + ReqToTokenPool.write + ContextDecodeLayout.from_layout,
  * akv/system/sglang/srt/context_system/occurrence.py:47-66,632-767 and

@@ -73,6 +73,7 @@ def test_gpt_oss_decode_after_drop_and_reposition(device):
     rows = torch.arange(B, dtype=torch.int64, device=device)
     tables.compact_rows(inputs, table, rows, fresh, out, generated=torch.ones(B, dtype=torch.int32, device=device),
                         birth_slots=birth)
+    tables.check_status(out)  # the lists feed the Reposition below
     pool = synth.make_pool(model, w.pool_slots, device, seed=9, generate_on_device=True)
     rope = synth.rope_table(w, device)
     ops.reposition_kv_layers(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], out.copy_src, out.copy_dst,

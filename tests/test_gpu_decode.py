@@ -148,6 +148,7 @@ def test_pipeline_compaction_feeds_registry(device):
     gen = torch.ones(w.n_requests, dtype=torch.int32, device=device)
     row_ids = torch.arange(w.n_requests, dtype=torch.int64, device=device)
     tables.compact_rows(inputs, table, row_ids, fresh, out, generated=gen)
+    tables.check_status(out)  # the decode layout feeds the index kernels below
     kept_off = np.concatenate(([0], np.cumsum(inputs.kept)))
     rows = []
     for b, lay in enumerate(layouts):

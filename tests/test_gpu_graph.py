@@ -47,6 +47,8 @@ def test_graph_replays_match_eager(device):
         page_table.context_decode_indices(registry, table, rows, seq, indptr, kv)
 
     dst = fresh.long()
+    tables.compact_rows(inputs, table, rows, fresh, out, generated=gen, birth_slots=birth)
+    tables.check_status(out)  # before any list reaches the Reposition
     step()
     torch.cuda.synchronize()
     want = [t.clone() for t in (table, out.retired, out.copy_src, out.copy_pairs, out.kv_indices, kv, indptr)]
