@@ -860,31 +860,36 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(const CompactArgs a) 
 //
 // A tile loads its inputs once, publishes its kept and moved counts (and,
 // for the requests that start in it, their counts before their first token;
-// retired counts follow from tokens - kept + moved), and arrives at
-// a barrier.  The last tile to arrive scans every tile's counts into the
-// exclusive prefixes and releases the others; each tile then writes its
-// outputs.  Arrivals are counted per group of tiles (tile mod groups), the
-// last of a group arriving at one top counter, so no address takes more than
-// about tiles / groups atomics; each group polls its own generation word.
-// Every counter is zero at rest: the last arrival of a group or at the top
-// resets it, so the workspace must be zero before its first use.  What
-// crosses tiles (counts, prefixes, barrier words, the status word) moves by
-// agent-scope atomic loads and stores, ordered by waiting for completion;
-// no cache-wide fence is needed.  Waits are
-// bounded: a tile that stops waiting cancels its group's generation word by
-// compare-and-swap, so a release and a withdrawal exclude each other, skips
-// its outputs, and the status word reads 3.  Tile 0 sets the status word to
-// 2 first, which the last arrival overwrites.  All tiles of one launch fit
-// on the device at once (the host checks occupancy), so waits end in
-// practice long before the bound.
+// retired counts follow from tokens - kept + moved) and arrives at its
+// group: 64 consecutive tiles.  The last tile to arrive in group k sums the
+// group's counts, publishes the group's totals, reads the totals of groups
+// 0 .. k-1 (one lane each), writes its tiles' exclusive prefixes and
+// releases the group; each tile then writes its outputs.  Groups release in
+// order as they fill, so the first tiles write while later ones still load.
+//
+// Per call every tile reads the epoch word E; group records and release
+// words carry the tag E + 1, so nothing but the arrival counters needs
+// resetting between calls; the last group's releaser advances E, after every
+// tile has read it.  Arrival counters are reset by each group's last
+// arrival, so the workspace must be zero before its first use.  What crosses
+// tiles (counts, prefixes, records, release words, the status word) moves by
+// agent-scope atomic loads and stores, ordered by waiting for completion; no
+// cache-wide fence is needed.  Waits are bounded: a tile that stops waiting
+// cancels its group's release word by compare-and-swap, so a release and a
+// withdrawal exclude each other; a withdrawn tile skips its outputs and sets
+// bit 2 of the status word.  Tile 0 sets the status word to 2 first; the last
+// group clears that bit when its look-back completes.  All tiles of one
+// launch fit on the device at once (the host checks occupancy), so waits end
+// in practice long before the bound.
 
-constexpr int kGroups = 32;
+constexpr int kGroupTiles = 64;  // tiles per group: one lane each
+constexpr int kMaxGroups = 32;
 constexpr int kSyncStride = 32;  // one 128-byte line per word
 constexpr uint32_t kCancelled = 0x80000000u;
+constexpr uint32_t kTagMask = 0x0fffffffu;
 constexpr uint32_t kPollLimit = 1u << 20;  // ~1 s of polling at most
-constexpr int kFusedScanPer = 8;
-constexpr int64_t kFusedMaxTiles = static_cast<int64_t>(kThreads) * kFusedScanPer;
-constexpr int64_t kSyncBytes = static_cast<int64_t>(2 * kGroups + 1) * kSyncStride * 4;
+constexpr int64_t kFusedMaxTiles = static_cast<int64_t>(kGroupTiles) * kMaxGroups;
+constexpr int64_t kSyncBytes = static_cast<int64_t>(3 * kMaxGroups + 1) * kSyncStride * 4;
 
 // Data that one tile writes and another reads within the launch goes through
 // agent-scope atomic loads and stores, which the device keeps coherent across
@@ -901,103 +906,121 @@ __device__ __forceinline__ int2 get_pair(const int2* p) {
 }
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8)); }
 
-__device__ __forceinline__ uint32_t* arrive_word(const CompactArgs& a, int g) { return a.sync + g * kSyncStride; }
-__device__ __forceinline__ uint32_t* top_word(const CompactArgs& a) { return a.sync + kGroups * kSyncStride; }
-__device__ __forceinline__ uint32_t* gen_word(const CompactArgs& a, int g) {
-  return a.sync + (kGroups + 1 + g) * kSyncStride;
+__device__ __forceinline__ uint32_t* arrive_word(const CompactArgs& a, int k) { return a.sync + k * kSyncStride; }
+__device__ __forceinline__ uint64_t* record_word(const CompactArgs& a, int k) {
+  return reinterpret_cast<uint64_t*>(a.sync + (kMaxGroups + k) * kSyncStride);
+}
+__device__ __forceinline__ uint32_t* release_word(const CompactArgs& a, int k) {
+  return a.sync + (2 * kMaxGroups + k) * kSyncStride;
+}
+__device__ __forceinline__ uint32_t* epoch_word(const CompactArgs& a) { return a.sync + 3 * kMaxGroups * kSyncStride; }
+
+// A group record: tag in bits 36..63, kept tokens in 18..35, moved in 0..17
+// (a group holds at most 64 x 2048 tokens).
+__device__ __forceinline__ uint64_t make_record(uint32_t tag, uint32_t kept, uint32_t moved) {
+  return (static_cast<uint64_t>(tag) << 36) | (static_cast<uint64_t>(kept) << 18) | moved;
 }
 
-// Thread 0: polls the group's generation word read before arriving (g).
-// True once the last tile has released the group; false when this tile
-// withdrew (the wait ran out) or another tile of the group withdrew.
-__device__ bool wait_release(uint32_t* gen, uint32_t g) {
+__device__ __forceinline__ void mark_withdrawn(const CompactArgs& a) {
+  if (a.status) __hip_atomic_fetch_or(reinterpret_cast<uint32_t*>(a.status), 4u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Thread 0 of a waiting tile: polls the group's release word, read as v0
+// before arriving.  True once released with `tag`; false when this tile
+// withdrew (the wait ran out) or the group was cancelled.
+__device__ bool wait_release(uint32_t* word, uint32_t v0, uint32_t tag) {
   for (uint32_t polls = 0;; ++polls) {
-    const uint32_t v = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (v != g) return v != (g | kCancelled);
+    const uint32_t v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (v != v0) return v == tag;
     if (polls >= kPollLimit) {
-      uint32_t expected = g;
-      if (__hip_atomic_compare_exchange_strong(gen, &expected, g | kCancelled, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+      uint32_t expected = v0;
+      if (__hip_atomic_compare_exchange_strong(word, &expected, tag | kCancelled, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT))
         return false;
-      return expected != (g | kCancelled);
+      return expected == tag;
     }
-    __builtin_amdgcn_s_sleep(4);
+    __builtin_amdgcn_s_sleep(2);
   }
 }
 
-// The last tile to arrive: exclusive (kept, moved) prefixes of every tile,
-// the status word, then the release of every group.  Each thread sums 8
-// consecutive tiles' packed counts (each half stays below 2^16).
+// Wave 0 of the last tile to arrive in group k: the group's totals, the
+// totals of every earlier group, its tiles' prefixes, the release.  Returns
+// (wave-uniform) whether the tiles' prefixes were written.
 template <int STEPS>
-__device__ void scan_and_release(const CompactArgs& a, const Tile<STEPS, true>& sh) {
-  constexpr int K = kFusedScanPer;
-  const int w = threadIdx.x >> 6;
-  const int64_t first = static_cast<int64_t>(threadIdx.x) * K;
-  uint32_t v[K];
-#pragma unroll
-  for (int u = 0; u < K; ++u) {
-    const int64_t i = first + u;
-    v[u] = __hip_atomic_load(a.tile_pack + (i < a.tiles ? i : a.tiles - 1), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-  }
-  uint32_t own = 0;
-#pragma unroll
-  for (int u = 0; u < K; ++u) own += first + u < a.tiles ? v[u] : 0u;
-  __shared__ int32_t part[kWaves][2];
-  int32_t pre[2], tot[2];
-  const int32_t mine[2] = {static_cast<int32_t>(own & 0xffffu), static_cast<int32_t>(own >> 16)};
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int32_t inc = __ockl_wfscan_add_i32(mine[c], true);
-    pre[c] = inc - mine[c];
-    if (lane_id() == 63) part[w][c] = inc;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    tot[c] = 0;
-    for (int q = 0; q < kWaves; ++q) {
-      if (q < w) pre[c] += part[q][c];
-      tot[c] += part[q][c];
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < K; ++u) {
-    if (first + u < a.tiles) {
-      put_pair(a.tile_pre + first + u, pre[0], pre[1]);
-      pre[0] += static_cast<int32_t>(v[u] & 0xffffu);
-      pre[1] += static_cast<int32_t>(v[u] >> 16);
-    }
-  }
-  if (threadIdx.x == 0) put_pair(a.tile_pre + a.tiles, tot[0], tot[1]);
-  const int64_t retired = a.total - tot[0] + tot[1];
-  const bool bad = tot[1] != a.fresh_count || tot[0] > a.kept_capacity || retired > a.retired_capacity ||
-                   (a.kv_indices && tot[0] + sh.s_genx[a.n_requests] > a.kv_capacity);
-  wait_stores();
-  __syncthreads();
-  if (w == 0) {
-    // release every group: at most one withdrawal can change a word first
-    const int groups = a.groups;
-    bool cancelled = false;
-    if (lane_id() < groups) {
-      uint32_t* gen = gen_word(a, lane_id());
-      uint32_t g = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      cancelled = true;  // stays so only if every attempt fails, which no withdrawal can cause
-      for (int k = 0; k < 3; ++k) {
-        const uint32_t next = ((g & ~kCancelled) + 1u) & ~kCancelled;
-        uint32_t expected = g;
-        if (__hip_atomic_compare_exchange_strong(gen, &expected, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT)) {
-          cancelled = (g & kCancelled) != 0;
-          break;
-        }
-        g = expected;
+__device__ bool release_group(const CompactArgs& a, const Tile<STEPS, true>& sh, int k, uint32_t tag, uint32_t epoch) {
+  const int lane = lane_id();
+  const int64_t first = static_cast<int64_t>(k) * kGroupTiles;
+  const int count = static_cast<int>(a.tiles - first < kGroupTiles ? a.tiles - first : kGroupTiles);
+  const int groups = a.groups;
+  // this group's tiles, one per lane
+  const uint32_t v =
+      __hip_atomic_load(a.tile_pack + first + (lane < count ? lane : count - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int32_t kt = lane < count ? static_cast<int32_t>(v & 0xffffu) : 0;
+  const int32_t mt = lane < count ? static_cast<int32_t>(v >> 16) : 0;
+  const int32_t k_in = __ockl_wfscan_add_i32(kt, false);
+  const int32_t m_in = __ockl_wfscan_add_i32(mt, false);
+  const int32_t k_sum = __shfl(k_in + kt, 63);
+  const int32_t m_sum = __shfl(m_in + mt, 63);
+  if (lane == 0)
+    __hip_atomic_store(record_word(a, k), make_record(tag, static_cast<uint32_t>(k_sum), static_cast<uint32_t>(m_sum)),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // look back: the totals of groups 0 .. k-1, one lane each
+  int64_t bk = 0, bm = 0;
+  bool ok = true;
+  if (lane < k) {
+    uint64_t rec = 0;
+    for (uint32_t polls = 0;; ++polls) {
+      rec = __hip_atomic_load(record_word(a, lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (static_cast<uint32_t>(rec >> 36) == tag) break;
+      if (polls >= kPollLimit) {
+        ok = false;
+        break;
       }
+      __builtin_amdgcn_s_sleep(2);
     }
-    const bool any = __ballot(cancelled) != 0;
-    if (lane_id() == 0 && a.status)
-      __hip_atomic_store(a.status, any ? 3 : (bad ? 1 : 0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bk = static_cast<int64_t>((rec >> 18) & 0x3ffffu);
+    bm = static_cast<int64_t>(rec & 0x3ffffu);
   }
+  const bool all_ok = __ballot(!ok) == 0;
+  const int64_t base_k = __ockl_wfred_add_i64(bk);
+  const int64_t base_m = __ockl_wfred_add_i64(bm);
+  if (all_ok) {
+    if (lane < count) put_pair(a.tile_pre + first + lane, static_cast<int32_t>(base_k + k_in), static_cast<int32_t>(base_m + m_in));
+    if (k == groups - 1 && lane == 0)
+      put_pair(a.tile_pre + a.tiles, static_cast<int32_t>(base_k + k_sum), static_cast<int32_t>(base_m + m_sum));
+    wait_stores();
+  }
+  if (lane == 0) {
+    // release (or cancel) the group: at most one withdrawal can change the word first
+    uint32_t* word = release_word(a, k);
+    uint32_t cur = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool cancelled = true;  // stays so only if every attempt fails, which no withdrawal can cause
+    for (int t = 0; t < 3; ++t) {
+      uint32_t expected = cur;
+      if (__hip_atomic_compare_exchange_strong(word, &expected, all_ok ? tag : (tag | kCancelled), __ATOMIC_RELAXED,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+        cancelled = cur == (tag | kCancelled);
+        break;
+      }
+      cur = expected;
+    }
+    if (!all_ok || cancelled) mark_withdrawn(a);
+    if (k == groups - 1) {
+      if (all_ok && a.status) {
+        // every tile has arrived: the status word's final size check
+        const int64_t kept = base_k + k_sum, moved = base_m + m_sum;
+        const int64_t retired = a.total - kept + moved;
+        const bool bad = moved != a.fresh_count || kept > a.kept_capacity || retired > a.retired_capacity ||
+                         (a.kv_indices && kept + sh.s_genx[a.n_requests] > a.kv_capacity);
+        uint32_t* st = reinterpret_cast<uint32_t*>(a.status);
+        __hip_atomic_fetch_and(st, ~2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (bad) __hip_atomic_fetch_or(st, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __hip_atomic_store(epoch_word(a), epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  return all_ok;
 }
 
 // Scalar registers are capped at 88 (86 reported): measured on MI355X, a
@@ -1009,15 +1032,17 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(88)))
   using T = Tile<STEPS, true>;
   __shared__ T sh;
   __shared__ Window win;
-  __shared__ uint32_t s_wait[2];  // [0]: 1 = last to arrive, 0 = wait; [1]: generation read before arriving
-  __shared__ uint32_t s_go;
+  __shared__ uint32_t s_sync[4];  // epoch, release word before arriving, role, go
   const int64_t tile = blockIdx.x;
   const int64_t t0 = tile * T::kTile;
   const int64_t t1 = t0 + T::kTile < a.total ? t0 + T::kTile : a.total;
   const int n = a.n_requests;
-  // status words are written by two tiles in order: coherent stores
-  if (tile == 0 && threadIdx.x == 0 && a.status)
-    __hip_atomic_store(a.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int k = static_cast<int>(tile / kGroupTiles);
+  if (threadIdx.x == 0) {
+    s_sync[0] = __hip_atomic_load(epoch_word(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // status bit 1 until the last group's look-back completes
+    if (tile == 0 && a.status) __hip_atomic_store(a.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   // one round of loads: the tile's inputs and flat birth slots, the batch's
   // request offsets, rows and generated counts
   uint8_t kb[STEPS];
@@ -1068,34 +1093,34 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(88)))
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   wait_stores();
   __syncthreads();
-  const int groups = a.groups;
-  const int gi = static_cast<int>(tile % groups);
+  const uint32_t epoch = s_sync[0];
+  const uint32_t tag = (epoch + 1u) & kTagMask;
   if (threadIdx.x == 0) {
-    // the generation is read (and the read complete) before arriving
-    const uint32_t g = __hip_atomic_load(gen_word(a, gi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the release word is read (and the read complete) before arriving
+    s_sync[1] = __hip_atomic_load(release_word(a, k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wait_stores();
-    const uint32_t gsize = static_cast<uint32_t>((a.tiles - gi + groups - 1) / groups);
+    const int64_t gfirst = static_cast<int64_t>(k) * kGroupTiles;
+    const uint32_t gsize = static_cast<uint32_t>(a.tiles - gfirst < kGroupTiles ? a.tiles - gfirst : kGroupTiles);
     uint32_t last = 0;
-    if (__hip_atomic_fetch_add(arrive_word(a, gi), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gsize - 1) {
-      __hip_atomic_store(arrive_word(a, gi), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (__hip_atomic_fetch_add(top_word(a), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-          static_cast<uint32_t>(groups) - 1) {
-        __hip_atomic_store(top_word(a), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = 1;
-      }
+    if (__hip_atomic_fetch_add(arrive_word(a, k), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gsize - 1) {
+      __hip_atomic_store(arrive_word(a, k), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = 1;
     }
-    s_wait[0] = last;
-    s_wait[1] = g;
+    s_sync[2] = last;
   }
   __syncthreads();
-  if (s_wait[0]) {
-    scan_and_release<STEPS>(a, sh);
-  } else {
-    if (threadIdx.x == 0) s_go = wait_release(gen_word(a, gi), s_wait[1]) ? 1u : 0u;
-    __syncthreads();
-    if (!s_go) return;
+  if (s_sync[2]) {
+    if (threadIdx.x < 64) {
+      const bool ok = release_group<STEPS>(a, sh, k, tag, epoch);
+      if (threadIdx.x == 0) s_sync[3] = ok ? 1u : 0u;
+    }
+  } else if (threadIdx.x == 0) {
+    const bool go = wait_release(release_word(a, k), s_sync[1], tag);
+    if (!go) mark_withdrawn(a);
+    s_sync[3] = go ? 1u : 0u;
   }
   __syncthreads();
+  if (!s_sync[3]) return;
   // the tile's prefix and, when a request spans in, its start counts
   const int2 pre = get_pair(a.tile_pre + tile);
   int64_t sums[kCounters];
@@ -1306,7 +1331,7 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
       const int64_t t = tile_count(total_tokens, kFusedSteps[v]);
       if (t > kFusedMaxTiles || t > fused_capacity(v)) continue;
       a.tiles = t;
-      a.groups = static_cast<int32_t>(t < kGroups ? t : kGroups);
+      a.groups = static_cast<int32_t>((t + kGroupTiles - 1) / kGroupTiles);
       launch_fused(kFusedSteps[v], a, st);
       return check_launch("akv_compact_rows");
     }

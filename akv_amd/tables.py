@@ -217,11 +217,11 @@ def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_po
     return outputs
 
 
-_STATUS_TEXT = {
-    1: "fresh slot count or an output capacity does not match the batch",
-    2: "the one-launch barrier did not complete (workspace not zero-filled before its first use?)",
-    3: "a tile stopped waiting at the one-launch barrier (tiles could not all run at once)",
-}
+_STATUS_BITS = (
+    (1, "fresh slot count or an output capacity does not match the batch"),
+    (2, "the one-launch barrier did not complete (workspace not zero-filled before its first use?)"),
+    (4, "a tile stopped waiting at the one-launch barrier (tiles could not all run at once)"),
+)
 
 
 def check_status(outputs):
@@ -230,7 +230,8 @@ def check_status(outputs):
     metadata.  Synchronises with the device (one 4-byte read)."""
     code = int(outputs.status.item())
     if code:
-        raise RuntimeError(f"akv_compact_rows status {code}: {_STATUS_TEXT.get(code, 'unknown')}")
+        why = "; ".join(text for bit, text in _STATUS_BITS if code & bit) or "unknown"
+        raise RuntimeError(f"akv_compact_rows status {code}: {why}")
     return outputs
 
 

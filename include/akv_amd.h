@@ -99,18 +99,20 @@ int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t total_tokens);
  *   kv_indptr  (opt.)   [B+1] exclusive scan of kept + generated
  *   last_page_len (opt.) [B] ((kept + generated - 1) % page_size) + 1, 0 if empty
  *   counts     (opt.)   [B,3] kept, moved, retired
- *   status     (opt.)   device int32: 0, or 1 if fresh_count or a capacity
- *                       does not match (outputs are then partial); 2 or 3
- *                       if the one-launch path's bounded wait ran out (a
- *                       workspace that was not zero-filled, or a device
- *                       shared so heavily that the tiles could not all
- *                       run at once; outputs are then partial)
+ *   status     (opt.)   device int32: 0, or bit 0 if fresh_count or a
+ *                       capacity does not match; bit 1 if the one-launch
+ *                       path's barrier did not complete and bit 2 if a tile
+ *                       stopped waiting at it (a workspace that was not
+ *                       zero-filled, or a device shared so heavily that the
+ *                       tiles could not all run at once).  Outputs are
+ *                       partial unless it reads 0.
  * retired, the copy lists and raw_indices / active_positions may be NULL
  * when retired_capacity, fresh_count and kept_capacity are 0.
  * One launch when the batch has at most 512 requests, fewer than 2^29
  * tokens (and list capacities) and some tile size lets every tile run on
  * the device at once
- * (tiles publish counts, the last to arrive scans them, all then write);
+ * (tiles publish counts; groups of 64 tiles are released in order, each
+ * by its last arrival after summing the earlier groups' totals);
  * otherwise two launches: per-tile counts, then per-tile prefixes and every
  * output.
  * Replaces the CPU numpy/H2D path of OccurrenceState.advance +
