@@ -1206,6 +1206,20 @@ int64_t fused_capacity(int v) {
   return c;
 }
 
+// The one-launch variant for a batch (index into kFusedSteps), or -1 when
+// it takes the two-launch path: more than kStagedRequests requests, a size
+// at or past 2^29 (32-bit byte offsets), or no tile size whose tiles all fit
+// on the current device.
+int fused_variant(int32_t n_requests, int64_t total_tokens, int64_t largest_list) {
+  constexpr int64_t kSmall = int64_t{1} << 29;
+  if (n_requests > kStagedRequests || total_tokens >= kSmall || largest_list >= kSmall) return -1;
+  for (int v = 0; v < kFusedVariants; ++v) {
+    const int64_t t = tile_count(total_tokens, kFusedSteps[v]);
+    if (t <= kFusedMaxTiles && t <= fused_capacity(v)) return v;
+  }
+  return -1;
+}
+
 void launch_fused(int steps, const CompactArgs& a, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(a.tiles));
   switch (steps) {
@@ -1241,6 +1255,13 @@ extern "C" int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t total
   using namespace akv;
   if (n_requests < 0 || total_tokens < 0) return -1;
   return workspace_layout(n_requests, total_tokens).bytes;
+}
+
+extern "C" int akv_compact_launches(int32_t n_requests, int64_t total_tokens, int64_t largest_list) {
+  using namespace akv;
+  if (n_requests < 0 || total_tokens < 0 || largest_list < 0) return fail(AKV_EINVAL, "akv_compact_launches: negative size");
+  if (n_requests == 0) return 0;
+  return fused_variant(n_requests, total_tokens, largest_list) >= 0 ? 1 : 2;
 }
 
 extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, int64_t total_tokens,
@@ -1323,18 +1344,15 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
   a.n_requests = n_requests;
 
   hipStream_t st = as_stream(stream);
-  constexpr int64_t kSmall = int64_t{1} << 29;  // 32-bit byte offsets of every output
-  if (n_requests <= kStagedRequests && total_tokens < kSmall && fresh_count < kSmall && retired_capacity < kSmall &&
-      kept_capacity < kSmall && (!kv_indices || kv_capacity < kSmall)) {
-    // one launch when a tile size exists whose tiles all fit on the device
-    for (int v = 0; v < kFusedVariants; ++v) {
-      const int64_t t = tile_count(total_tokens, kFusedSteps[v]);
-      if (t > kFusedMaxTiles || t > fused_capacity(v)) continue;
-      a.tiles = t;
-      a.groups = static_cast<int32_t>((t + kGroupTiles - 1) / kGroupTiles);
-      launch_fused(kFusedSteps[v], a, st);
-      return check_launch("akv_compact_rows");
-    }
+  int64_t largest = fresh_count > retired_capacity ? fresh_count : retired_capacity;
+  if (kept_capacity > largest) largest = kept_capacity;
+  if (kv_indices && kv_capacity > largest) largest = kv_capacity;
+  const int v = fused_variant(n_requests, total_tokens, largest);
+  if (v >= 0) {
+    a.tiles = tile_count(total_tokens, kFusedSteps[v]);
+    a.groups = static_cast<int32_t>((a.tiles + kGroupTiles - 1) / kGroupTiles);
+    launch_fused(kFusedSteps[v], a, st);
+    return check_launch("akv_compact_rows");
   }
   switch (steps) {
     case 1:

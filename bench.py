@@ -37,7 +37,7 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from akv_amd import ops, synth, tables  # noqa: E402
+from akv_amd import _lib, ops, synth, tables  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "Reposition retained-KV GB/s (% HBM peak) + p50 latency, 32k GPT-OSS-shaped"
@@ -193,7 +193,8 @@ def tiny_config(device, flush):
         "workload": pipe.w.name, "tokens": pipe.n, "moved": pipe.moved,
         "step_ms_back_to_back": round(warm, 5), "step_ms_graph_replay": round(graph, 5),
         "step_p50_ms": round(percentile(cold, 50), 5),
-        "step_p99_ms": round(percentile(cold, 99), 5), "kernel_launches_per_step": 3,
+        "step_p99_ms": round(percentile(cold, 99), 5),
+        "kernel_launches_per_step": compaction_launches(pipe.inputs) + 1,
     }
 
 
@@ -263,7 +264,7 @@ def ragged_config(device, flush):
         "moved": inputs.moved_total, "step_ms_back_to_back": round(warm, 5),
         "step_ms_graph_replay": round(graph, 5),
         "step_p50_ms": round(percentile(cold, 50), 5), "step_p99_ms": round(percentile(cold, 99), 5),
-        "kernel_launches_per_step": 2,
+        "kernel_launches_per_step": compaction_launches(inputs),
         "metadata_bytes": meta, "host_event_compile_ms": round(compile_ms, 1),
     }
 
@@ -884,6 +885,12 @@ def _chunked_ownership_port():
     return time.perf_counter() - t0
 
 
+def compaction_launches(inputs):
+    """Kernel launches akv_compact_rows makes for this batch on this device."""
+    total = sum(inputs.n_tokens)
+    return int(_lib.load().akv_compact_launches(inputs.n_requests, total, total + inputs.n_requests))
+
+
 def host_info(threads):
     """lscpu model name and core counts of this host."""
     info = {}
@@ -1041,7 +1048,7 @@ def main():
         "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         # compaction: count + scatter; Reposition: one launch for the
         # 36-layer group
-        "kernel_launches_per_step": 1 if args.reposition_only else 3,
+        "kernel_launches_per_step": 1 if args.reposition_only else compaction_launches(pipe.inputs) + 1,
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),

@@ -79,6 +79,17 @@ int akv_reposition_kv_layers(const uint64_t* k_ptrs, const uint64_t* v_ptrs,
 int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t total_tokens);
 
 /*
+ * Kernel launches akv_compact_rows makes on the current device for a batch
+ * of n_requests holding total_tokens raw tokens whose largest list (fresh
+ * slots, retired / kept / kv_indices capacity) holds largest_list entries:
+ * 1 (one launch, every tile resident at once) or 2; 0 for an empty batch,
+ * AKV_EINVAL for negative sizes.  No device work.  No counterpart in the
+ * reference: it tells a caller which path (and which status bits) to expect.
+ */
+int akv_compact_launches(int32_t n_requests, int64_t total_tokens,
+                         int64_t largest_list);
+
+/*
  * Batched page-table compaction of a single-owner final forward.  For
  * request b, raw tokens [req_offsets[b], req_offsets[b+1]) of the flat
  * keep / birth_positions / final_positions vectors (req_offsets[B] ==

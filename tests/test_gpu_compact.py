@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from akv_amd import synth, tables
+from akv_amd import _lib, synth, tables
 from oracle import occurrence as occ
 
 pytestmark = pytest.mark.gpu
@@ -180,9 +180,22 @@ def test_requests_denser_than_the_tile_window(device):
     _run(device, w, generated=[int(x) for x in np.random.default_rng(31).integers(0, 3, size=n)])
 
 
+def test_launch_paths(device):
+    """Which path each batch shape takes on this device: one launch while every
+    tile fits at once and the batch stages in LDS, two launches otherwise."""
+    lib = _lib.load()
+    assert lib.akv_compact_launches(64, 2_118_412, 2_118_412) == 1  # the ragged batch
+    assert lib.akv_compact_launches(1, 32_768, 32_768) == 1
+    assert lib.akv_compact_launches(32, 32 * 32_768, 32 * 32_768) == 1
+    assert lib.akv_compact_launches(80, 80 * 65_536, 80 * 65_536) == 2  # more tiles than fit at once
+    assert lib.akv_compact_launches(5000, 200_000, 200_000) == 2  # more requests than LDS staging
+    assert lib.akv_compact_launches(4, 1000, 1 << 29) == 2  # a list past 32-bit byte offsets
+    assert lib.akv_compact_launches(0, 0, 0) == 0
+
+
 def test_prefix_over_many_tiles(device):
-    # 80 x 64k tokens: 5000+ tiles of 1024 tokens, each summing the
-    # aggregates of up to 5000 earlier tiles
+    # 80 x 64k tokens (two-launch path): 5000+ tiles of 1024 tokens, each
+    # summing the aggregates of up to 5000 earlier tiles
     rng = np.random.default_rng(41)
     lengths = tuple([65536] * 80)
     spans = tuple(((int(a), int(a) + int(rng.integers(1, 5000))),) for a in rng.integers(0, 60000, size=80))
