@@ -29,7 +29,7 @@ _SIGNATURES = {
          c_int64, _P, _P, _P, c_int64, c_int64, _P, c_int32, c_int64, c_int32, c_int32, _P],
     ),
     "akv_compact_workspace_bytes": (c_int64, [c_int32, c_int64]),
-    "akv_compact_launches": (c_int32, [c_int32, c_int64, c_int64]),
+    "akv_compact_launches": (c_int32, [c_int32, c_int64, c_int64, _P]),
     "akv_compact_rows": (
         c_int32,
         [c_int32, _P, c_int64, _P, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64, _P, c_int64,

@@ -1257,11 +1257,15 @@ extern "C" int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t total
   return workspace_layout(n_requests, total_tokens).bytes;
 }
 
-extern "C" int akv_compact_launches(int32_t n_requests, int64_t total_tokens, int64_t largest_list) {
+extern "C" int akv_compact_launches(int32_t n_requests, int64_t total_tokens, int64_t largest_list,
+                                    int64_t* tile_tokens) {
   using namespace akv;
   if (n_requests < 0 || total_tokens < 0 || largest_list < 0) return fail(AKV_EINVAL, "akv_compact_launches: negative size");
+  if (tile_tokens) *tile_tokens = 0;
   if (n_requests == 0) return 0;
-  return fused_variant(n_requests, total_tokens, largest_list) >= 0 ? 1 : 2;
+  const int v = fused_variant(n_requests, total_tokens, largest_list);
+  if (tile_tokens) *tile_tokens = static_cast<int64_t>(kThreads) * (v >= 0 ? kFusedSteps[v] : tile_steps(total_tokens));
+  return v >= 0 ? 1 : 2;
 }
 
 extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, int64_t total_tokens,

@@ -888,7 +888,7 @@ def _chunked_ownership_port():
 def compaction_launches(inputs):
     """Kernel launches akv_compact_rows makes for this batch on this device."""
     total = sum(inputs.n_tokens)
-    return int(_lib.load().akv_compact_launches(inputs.n_requests, total, total + inputs.n_requests))
+    return int(_lib.load().akv_compact_launches(inputs.n_requests, total, total + inputs.n_requests, None))
 
 
 def host_info(threads):

@@ -83,11 +83,13 @@ int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t total_tokens);
  * of n_requests holding total_tokens raw tokens whose largest list (fresh
  * slots, retired / kept / kv_indices capacity) holds largest_list entries:
  * 1 (one launch, every tile resident at once) or 2; 0 for an empty batch,
- * AKV_EINVAL for negative sizes.  No device work.  No counterpart in the
- * reference: it tells a caller which path (and which status bits) to expect.
+ * AKV_EINVAL for negative sizes.  When tile_tokens is not NULL it receives
+ * the tokens per tile of that path (0 for an empty batch).  No device work.
+ * No counterpart in the reference: it tells a caller which path (and which
+ * status bits) to expect.
  */
 int akv_compact_launches(int32_t n_requests, int64_t total_tokens,
-                         int64_t largest_list);
+                         int64_t largest_list, int64_t* tile_tokens);
 
 /*
  * Batched page-table compaction of a single-owner final forward.  For

@@ -46,8 +46,8 @@ def test_validation_rejects_before_any_device_work(lib):
             args[int(i[1:])] = v
         return args
 
-    assert lib.akv_compact_launches(-1, 0, 0) == _lib.AKV_EINVAL
-    assert lib.akv_compact_launches(0, 0, 0) == 0
+    assert lib.akv_compact_launches(-1, 0, 0, None) == _lib.AKV_EINVAL
+    assert lib.akv_compact_launches(0, 0, 0, None) == 0
     assert lib.akv_compact_rows(*zeros(lib.akv_compact_rows, a0=-1)) == _lib.AKV_EINVAL
     assert lib.akv_compact_rows(*zeros(lib.akv_compact_rows, a0=2)) == _lib.AKV_EINVAL
     assert "null device pointer" in _lib.last_error()

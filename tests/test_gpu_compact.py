@@ -4,6 +4,8 @@ Integer outputs must be bit-exact: terminal rows (in place), retired slots,
 copy lists, decode layouts, compacted rows / kv_indices and kv_indptr.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -180,17 +182,62 @@ def test_requests_denser_than_the_tile_window(device):
     _run(device, w, generated=[int(x) for x in np.random.default_rng(31).integers(0, 3, size=n)])
 
 
+def _path(lib, n_requests, total, largest=None):
+    tile = ctypes.c_int64(0)
+    launches = lib.akv_compact_launches(n_requests, total, total + n_requests if largest is None else largest,
+                                        ctypes.byref(tile))
+    return launches, tile.value
+
+
 def test_launch_paths(device):
     """Which path each batch shape takes on this device: one launch while every
     tile fits at once and the batch stages in LDS, two launches otherwise."""
     lib = _lib.load()
-    assert lib.akv_compact_launches(64, 2_118_412, 2_118_412) == 1  # the ragged batch
-    assert lib.akv_compact_launches(1, 32_768, 32_768) == 1
-    assert lib.akv_compact_launches(32, 32 * 32_768, 32 * 32_768) == 1
-    assert lib.akv_compact_launches(80, 80 * 65_536, 80 * 65_536) == 2  # more tiles than fit at once
-    assert lib.akv_compact_launches(5000, 200_000, 200_000) == 2  # more requests than LDS staging
-    assert lib.akv_compact_launches(4, 1000, 1 << 29) == 2  # a list past 32-bit byte offsets
-    assert lib.akv_compact_launches(0, 0, 0) == 0
+    assert _path(lib, 64, 2_118_412)[0] == 1  # the ragged batch
+    assert _path(lib, 1, 32_768) == (1, 256)
+    assert _path(lib, 32, 32 * 32_768)[0] == 1
+    assert _path(lib, 80, 80 * 65_536) == (2, 1024)  # more tiles than fit at once
+    assert _path(lib, 5000, 200_000) == (2, 256)  # more requests than LDS staging
+    assert _path(lib, 4, 1000, 1 << 29)[0] == 2  # a list past 32-bit byte offsets
+    assert _path(lib, 0, 0) == (0, 0)
+
+
+def _batch_for(lib, n_requests, want, seed):
+    """A batch of n_requests whose path is `want` = (launches, tile tokens):
+    the middle of the range of totals that map to it (searched on the host)."""
+    hits = [t for t in range(8192, 3_200_000, 8192) if _path(lib, n_requests, t) == want]
+    if not hits:
+        pytest.skip(f"no batch of {n_requests} requests takes path {want} on this device")
+    total = hits[len(hits) // 2]
+    rng = np.random.default_rng(seed)
+    cuts = np.sort(rng.choice(np.arange(1, total), size=n_requests - 1, replace=False))
+    lengths = np.diff(np.concatenate(([0], cuts, [total])))
+    spans = []
+    for n in lengths:
+        n = int(n)
+        k = int(rng.integers(0, 3)) if n > 8 else 0
+        starts = np.sort(rng.choice(np.arange(n - 1), size=k, replace=False)) if k else []
+        req, prev = [], 0
+        for a in starts:
+            a = max(int(a), prev + 1 if req else 0)  # ordered, disjoint, not touching
+            b = min(n, a + 1 + int(rng.integers(0, max(1, n // 8))))
+            if a < b:
+                req.append((a, b))
+                prev = b
+        spans.append(tuple(req))
+    return synth.Workload(f"path-{want[0]}x{want[1]}", synth.TINY, tuple(int(n) for n in lengths), tuple(spans),
+                          seed=seed, table_positions=int(lengths.max()) + 8, pool_slots=3 * total + 1)
+
+
+# every tile size of the one-launch path, and of the two-launch path
+@pytest.mark.parametrize("n_requests,want", [(48, (1, 256 * st)) for st in (1, 2, 3, 4, 5, 6, 8)]
+                         + [(600, (2, 256)), (600, (2, 512)), (600, (2, 1024))])
+def test_every_tile_size(device, n_requests, want):
+    lib = _lib.load()
+    w = _batch_for(lib, n_requests, want, seed=want[1] + n_requests)
+    print(f"tile size {want} with {n_requests} requests, {sum(w.lengths)} tokens", flush=True)
+    assert _path(lib, w.n_requests, sum(w.lengths)) == want
+    _run(device, w, generated=[1] * w.n_requests)
 
 
 def test_prefix_over_many_tiles(device):
