@@ -20,6 +20,8 @@
 // instruction for the 8 x 64 bf16 head layout.  Layers whose base address is
 // not 16-byte aligned take an element-wise path inside the same kernel; other
 // shapes go to a generic element-per-thread kernel.
+#include <atomic>
+
 #include "common.h"
 
 namespace akv {
@@ -41,6 +43,9 @@ struct RepositionArgs {
   int32_t lanes_per_row;   // n_heads * units_per_head
   int32_t rows_per_block;  // layers processed side by side by one token
   int32_t tokens_per_block;
+  int64_t whole_tokens;    // tokens [0, whole_tokens) take one workgroup over
+                           // every layer; each later token one workgroup per
+                           // rows_per_block layers (one token per workgroup)
   int64_t n_tokens;
 };
 
@@ -319,7 +324,19 @@ __global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionAr
   const int local = threadIdx.x - slot * row_threads;
   const int row_sub = local / lpr;
   const int j = local - row_sub * lpr;
-  const int64_t token = static_cast<int64_t>(blockIdx.x) * a.tokens_per_block + slot;
+  // the launch's last tokens are cut into one workgroup per group of
+  // rows_per_block layers, so its tail is made of short workgroups
+  int64_t token;
+  int lbeg = 0, lend = a.n_layers;
+  if (static_cast<int64_t>(blockIdx.x) < a.whole_tokens || a.tokens_per_block != 1) {
+    token = static_cast<int64_t>(blockIdx.x) * a.tokens_per_block + slot;
+  } else {
+    const int parts = (a.n_layers + a.rows_per_block - 1) / a.rows_per_block;
+    const int64_t u = static_cast<int64_t>(blockIdx.x) - a.whole_tokens;
+    token = a.whole_tokens + u / parts;
+    lbeg = static_cast<int>(u % parts) * a.rows_per_block;
+    lend = lbeg + a.rows_per_block < a.n_layers ? lbeg + a.rows_per_block : a.n_layers;
+  }
   const int half = a.rotary_dim >> 1;
   const int cstride = coef_stride(half);
   float* coef = reinterpret_cast<float*>(coef_lds) + slot * 5 * cstride;
@@ -365,7 +382,7 @@ __global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionAr
   }
   __syncthreads();
   const bool aligned = !any_misaligned;
-  if (!live || row_sub >= a.n_layers) return;
+  if (!live || lbeg + row_sub >= lend) return;
 
   constexpr int64_t B = sizeof(T);
   mv.k_src = src * a.k_stride_slot * B;
@@ -391,10 +408,10 @@ __global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionAr
   // one row in flight per lane: measured faster than prefetching the next
   // layer's row (fewer registers, more resident waves)
   if (aligned) {
-    for (int layer = row_sub; layer < a.n_layers; layer += a.rows_per_block)
+    for (int layer = lbeg + row_sub; layer < lend; layer += a.rows_per_block)
       mv.template finish<true>(mv.template load<true>(layer));
   } else {
-    for (int layer = row_sub; layer < a.n_layers; layer += a.rows_per_block)
+    for (int layer = lbeg + row_sub; layer < lend; layer += a.rows_per_block)
       mv.template finish<false>(mv.template load<false>(layer));
   }
 }
@@ -458,6 +475,8 @@ __global__ void __launch_bounds__(256) reposition_generic_kernel(const Repositio
 // beat 192 threads with the next layer prefetched, 576 threads, and several
 // tokens per workgroup; tokens whose rows fill less than two waves share a
 // workgroup.
+constexpr int kMaxDevices = 64;
+
 void geometry(RepositionArgs& a) {
   const int lpr = a.lanes_per_row;
   int rows = 384 / lpr;
@@ -473,6 +492,22 @@ void geometry(RepositionArgs& a) {
   a.tokens_per_block = tokens;
 }
 
+// Workgroups of `kernel` resident at once on the current device (0 when the
+// query fails), cached per device in `cache`.
+int64_t resident_workgroups(const void* kernel, int threads, size_t lds, std::atomic<int64_t>* cache) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int64_t c = cache[dev].load(std::memory_order_relaxed);
+  if (c > 0) return c;
+  int blocks = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, threads, lds) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  c = static_cast<int64_t>(blocks) * cus;
+  cache[dev].store(c, std::memory_order_relaxed);
+  return c;
+}
+
 template <typename T, typename CS>
 int launch_typed(RepositionArgs a, int64_t n_tokens, hipStream_t stream, bool vec_ok) {
   constexpr int VEC = Elem<T>::kVec;
@@ -482,20 +517,26 @@ int launch_typed(RepositionArgs a, int64_t n_tokens, hipStream_t stream, bool ve
     a.lanes_per_row = a.n_heads * a.units_per_head;
     geometry(a);
     const int threads = a.lanes_per_row * a.rows_per_block * a.tokens_per_block;
-    const dim3 grid(static_cast<unsigned>((n_tokens + a.tokens_per_block - 1) / a.tokens_per_block));
     const size_t lds = static_cast<size_t>(a.tokens_per_block) * 5 * coef_stride(a.rotary_dim >> 1) * sizeof(float);
     const bool wide = a.rotary_dim < a.head_dim || a.n_heads * (a.head_dim / VEC) > 2 * a.lanes_per_row;
-    if (a.is_neox) {
-      if (wide)
-        hipLaunchKernelGGL((reposition_vec_kernel<T, CS, true, true>), grid, dim3(threads), lds, stream, a);
-      else
-        hipLaunchKernelGGL((reposition_vec_kernel<T, CS, true, false>), grid, dim3(threads), lds, stream, a);
-    } else {
-      if (wide)
-        hipLaunchKernelGGL((reposition_vec_kernel<T, CS, false, true>), grid, dim3(threads), lds, stream, a);
-      else
-        hipLaunchKernelGGL((reposition_vec_kernel<T, CS, false, false>), grid, dim3(threads), lds, stream, a);
+    void (*kernel)(RepositionArgs) =
+        a.is_neox ? (wide ? reposition_vec_kernel<T, CS, true, true> : reposition_vec_kernel<T, CS, true, false>)
+                  : (wide ? reposition_vec_kernel<T, CS, false, true> : reposition_vec_kernel<T, CS, false, false>);
+    // the last tokens -- one device-full of workgroups -- each take one
+    // workgroup per pass, so the launch does not end on a partial round of
+    // full-length workgroups
+    int64_t units = (n_tokens + a.tokens_per_block - 1) / a.tokens_per_block;
+    a.whole_tokens = n_tokens;
+    const int parts = (a.n_layers + a.rows_per_block - 1) / a.rows_per_block;
+    if (a.tokens_per_block == 1 && parts > 1) {
+      static std::atomic<int64_t> cache[2][2][kMaxDevices];
+      int64_t tail = resident_workgroups(reinterpret_cast<const void*>(kernel), threads, lds,
+                                         cache[a.is_neox ? 1 : 0][wide ? 1 : 0]);
+      if (tail > n_tokens) tail = n_tokens;
+      a.whole_tokens = n_tokens - tail;
+      units = a.whole_tokens + tail * parts;
     }
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(units)), dim3(threads), lds, stream, a);
     return check_launch("akv_reposition_kv_layers");
   }
   const int64_t total = n_tokens * a.n_layers * a.n_heads * a.head_dim;
