@@ -10,20 +10,21 @@
 // active row of request_active_slots
 // (akv/system/sglang/srt/disaggregation/context_transfer.py:110-128).
 //
-// Two launches over tiles of 256 x STEPS tokens of the concatenated batch
-// (STEPS grows until the batch is about 2048 tiles):
-//   count    per tile: its kept / moved / retired counts and the generated
-//            entries of the requests that start in it (its aggregate); per
-//            request: the tile's counts before the request's first token
-//            and the request's raw row (two tiles per workgroup);
-//   scatter  per tile: its exclusive prefix, summed from every earlier
-//            tile's aggregate (16 bytes each, read in one unrolled batch of
-//            up to 2304 issued with the tile's own inputs), then every
-//            output the tile owns.
-// No workgroup waits for another and the workspace needs no clearing.  A
-// single-pass scan with decoupled look-back measured slower on this batch:
-// per-tile chains of dependent global round trips (publish, poll, read)
-// cost ~10 us under load, and 2048 tiles do not all fit on the chip at once.
+// Tiles of 256 x STEPS tokens of the concatenated batch, one of two paths:
+//   one launch (fused_kernel; at most 512 requests, fewer than 2^29 tokens,
+//            and a tile size whose tiles all fit on the device at once):
+//            each tile loads its inputs once, publishes its counts, and
+//            groups of 64 consecutive tiles are released in order by their
+//            last arrival (see the one-launch section below);
+//   two launches (count_kernel, scatter_kernel; every other batch, STEPS
+//            growing until the batch is about 2048 tiles): per-tile
+//            aggregates, then each tile sums every earlier tile's aggregate
+//            (16 bytes each, read in one unrolled batch of up to 2304 issued
+//            with the tile's own inputs) and writes every output it owns.
+// Both write their outputs through tile_outputs.  A single-pass scan with a
+// per-tile decoupled look-back measured slower on the ragged batch: per-tile
+// chains of dependent global round trips (publish, poll, read) cost ~10 us
+// under load, and 2048 tiles do not all fit on the chip at once.
 //
 // Loads are unconditional, from indices clamped into range, with the value
 // selected afterwards: a load under a divergent condition is followed by a
