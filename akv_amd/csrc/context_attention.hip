@@ -27,11 +27,19 @@
 // with global_load_lds_dwordx4 -- no staging registers -- and the slots of
 // the tile after it are fetched, all during this tile's math), for a wave's
 // W rows:
-//   S^T[64 keys x W rows] = K . Q^T           v_mfma_f32_16x16x32_bf16
-//   online softmax per row (column of S^T) in the exp2 domain, the running
-//   maximum moving only when a tile exceeds it by 2^8 (lazy rescale)
+//   S^T[64 keys x W rows] = K . Q^T - m       v_mfma_f32_16x16x32_bf16
+//     (Q carries the softmax scale in the log2 domain; the accumulator
+//     starts at each row's -m, so the scores leave the matrix cores ready
+//     for exp2)
+//   P^T = 2^(S^T) in bf16
+//   l[rows] = 1^T . P^T                       (row sums of the same bf16 P)
 //   O^T[D x W rows] += V^T . P^T              v_mfma_f32_16x16x32_bf16
-//   l[rows] += 1^T . P^T                      (row sums of the same bf16 P)
+// Online softmax without per-tile maxima: a row's running maximum m comes
+// from exact row maxima while the row has seen no key, then stays put; a
+// tile whose weight sum passes 2^32 (a score ~26 above m, or inf) is
+// computed again with exact maxima (moving m by the lazy rule: only when
+// the tile exceeds it by 2^8), and a running sum that passes 2^32 over many
+// tiles is renormalised by a power of two.
 // P^T leaves the first MFMA in the B-operand layout of the second (any
 // consistent split of the 32-long k axis over lanes gives the same product:
 // lane l uses keys 4(l/16)+i of two 16-key subtiles); V^T comes from the
@@ -43,7 +51,6 @@
 // D[4(l/16)+i][l%16]; ds_read_b64_tr_b16 -- within each 16-lane group, lane
 // j receives element j%4 of the 8-byte rows read by lanes j/4 + 4i, i < 4.
 #include <cmath>
-#include <type_traits>
 
 #include "common.h"
 
@@ -66,7 +73,9 @@ constexpr int rows_per_block(int d) { return 4 * 16 * sub_tiles(d); }  // (token
 constexpr int kThreads = 256;
 constexpr int kKeys = 64;  // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLazy = 8.f;  // log2-domain slack before the running maximum moves
+constexpr float kLazy = 8.f;  // log2-domain slack before an exact maximum moves
+constexpr float kBig = 4294967296.f;  // 2^32: a weight sum above it is renormalised
+constexpr float kHuge = 18446744073709551616.f;  // 2^64: above it the product may have overflowed
 
 struct CtxArgs {
   const __bf16* q;
@@ -87,7 +96,7 @@ struct CtxArgs {
   int32_t window;
   float scale_log2;
   int32_t out_f32;
-  int32_t group, tokens_per_block, kv_heads;
+  int32_t group, group_shift, tokens_per_block, kv_heads;
 };
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -243,25 +252,29 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
     return it < n_pref ? p_lo + it * kKeys : e_lo + (it - n_pref) * kKeys;
   };
 
-  // this lane's rows: row subtile s covers rows wave * 16 kSub + 16s + col
-  // per row subtile: (token within the block) | (q head << 16), and the
-  // row's position relative to qbase
-  int32_t row_th[kSub], row_rel[kSub];
+  // this lane's rows: row subtile s covers rows wave * 16 kSub + 16s + col,
+  // row r = (token r >> group_shift, q head g G + r % G); the rows'
+  // positions relative to qbase wait in LDS for the masked tiles
+  __shared__ int32_t rel_rows[rows_per_block(D)];
+  auto row_of = [&](int s) { return wave * (16 * kSub) + 16 * s + col; };
   bf16x8 qop[kSub][kKSteps];
 #pragma unroll
   for (int s = 0; s < kSub; ++s) {
-    const int r = wave * (16 * kSub) + 16 * s + col;
-    const int tl = r / G;
-    const int head = g * G + (r - tl * G);
-    row_th[s] = tl | (head << 16);
+    const int r = row_of(s);
+    const int tl = r >> a.group_shift;
+    const int head = g * G + (r & (G - 1));
     const bool ok = t0 + tl < qlen;
-    row_rel[s] = ok ? rel_pos(qpos_of(t0 + tl), qbase) : last_rel;
+    if (quad == 0) rel_rows[r] = ok ? rel_pos(qpos_of(t0 + tl), qbase) : last_rel;
 #pragma unroll
     for (int ks = 0; ks < kKSteps; ++ks) {
       u32x4 w = {0u, 0u, 0u, 0u};
       if (ok)
         w = load16(a.q + (qo0 + t0 + tl) * a.q_st + static_cast<int64_t>(head) * a.q_sh + 32 * ks + 8 * quad);
-      qop[s][ks] = __builtin_bit_cast(bf16x8, w);
+      // the softmax scale in the log2 domain is folded into Q (one bf16
+      // rounding), so the scores leave the matrix cores ready for exp2
+      const bf16x8 raw = __builtin_bit_cast(bf16x8, w);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qop[s][ks][i] = static_cast<__bf16>(static_cast<float>(raw[i]) * a.scale_log2);
     }
   }
 
@@ -273,8 +286,9 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   // blocks of K and of V.  Prefix slots are fetched one tile ahead.
   constexpr int kRowsPerBlock = 1024 / (2 * D);
   constexpr int kBlocksPerWave = kKeys / kRowsPerBlock / 4;
-  using SlotT = typename std::conditional<sizeof(IdxT) == 4, uint32_t, int64_t>::type;
-  SlotT slot[kBlocksPerWave];
+  // slot indices are below 2^32 (a pool of 2^32 slots of one 64-wide bf16
+  // head is 512 GiB): int64 indices address rows through their low 32 bits
+  uint32_t slot[kBlocksPerWave];
   int64_t preg = 0;  // raw position of key tid of the staged tile
   bool pvalid = false;
   const int my_row = lane / kChunks;   // row within a block
@@ -285,7 +299,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
 #pragma unroll
     for (int u = 0; u < kBlocksPerWave; ++u) {
       const int32_t j = base + (kBlocksPerWave * wave + u) * kRowsPerBlock + my_row;
-      slot[u] = static_cast<SlotT>(slots[j < plen ? j : plen - 1]);
+      slot[u] = static_cast<uint32_t>(slots[j < plen ? j : plen - 1]);
     }
   };
   auto stage = [&](int it, TileLds<D>& t) {
@@ -303,13 +317,10 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
         const uint64_t off = static_cast<uint32_t>(j < e_hi ? j : e_hi - 1);
         krow = kext_b + off * ke_sb;
         vrow = vext_b + off * ve_sb;
-      } else if constexpr (sizeof(IdxT) == 4) {
-        const uint64_t so = static_cast<uint32_t>(slot[u]);
+      } else {
+        const uint64_t so = slot[u];
         krow = kpool_b + so * kp_sb;
         vrow = vpool_b + so * vp_sb;
-      } else {
-        krow = reinterpret_cast<const char*>(kpool + slot[u] * a.kp_ss);
-        vrow = reinterpret_cast<const char*>(vpool + slot[u] * a.vp_ss);
       }
       __builtin_amdgcn_global_load_lds(krow + 16 * ck, (lds_void*)(&t.k[blk * kRowsPerBlock][0]), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(vrow + 16 * cv, (lds_void*)(&t.v[blk * kRowsPerBlock][0]), 16, 0, 0);
@@ -331,20 +342,28 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   };
 
   f32x4 oacc[kDTiles][kSub];
+  // per row: the negated running maximum -m (log2 domain) in all four
+  // entries of a quad that the score MFMAs accumulate onto, so the scores
+  // leave the matrix cores as t - m, and the running sum of the bf16 weights
+  // (4 equal copies); a row with a zero sum has seen no key (its quad holds 0)
+  f32x4 neg_m[kSub], lacc[kSub];
+  auto clear_rows = [&]() {
 #pragma unroll
-  for (int dt = 0; dt < kDTiles; ++dt)
+    for (int s = 0; s < kSub; ++s) {
+      neg_m[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+      lacc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < kSub; ++s) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // per row: the reference maximum m_run (log2 domain), its negation as the
-  // exp2 shift (0 while the row has seen no key), and the raw-score level
-  // above which a tile moves it, (m_run + kLazy) / scale -- all three change
-  // only when the maximum moves
-  float m_run[kSub], neg_m[kSub], bump_at[kSub];
-#pragma unroll
-  for (int s = 0; s < kSub; ++s) m_run[s] = -INFINITY, neg_m[s] = 0.f, bump_at[s] = -INFINITY;
-  f32x4 lacc[kSub];  // row sums (4 equal copies)
-#pragma unroll
-  for (int s = 0; s < kSub; ++s) lacc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  clear_rows();
+  // some row of this wave has seen no key yet (uniform): tiles take the
+  // exact row maxima until every row has a maximum
+  bool unset = true;
+  // after a restart every tile takes the exact maxima (uniform)
+  bool exact_all = false;
+  __shared__ int32_t restart_flag;
+  if (tid == 0) restart_flag = 0;
   const bf16x8 kOnes = {__bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f),
                         __bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f)};
 
@@ -368,93 +387,96 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
     const int32_t pos0 = __builtin_amdgcn_readfirstlane(cur.pos[0]);
     const bool masked = count < kKeys || (ext && base + kKeys - 1 > t0) ||
                         (a.window >= 0 && pos0 < last_rel - a.window);
+    const bool exact = unset || exact_all;
 
-    // S^T = K . Q^T
-    f32x4 sacc[4][kSub];
+    // The tile in two halves of 32 keys (kk), each complete before the next:
+    //   S^T = K . Q^T - m      (Q carries the scale: log2 domain; the first
+    //                           k-step accumulates onto -m)
+    //   P^T = 2^(S^T) in bf16  (the B operand of both products)
+    //   l += 1^T . P^T         (row sums of the same bf16 weights on the
+    //                           matrix cores: O stays a convex combination)
+    //   O^T += V^T . P^T
+    // Masked tiles add the mask (masked scores become -inf in place: exp2 ->
+    // 0); exact tiles the row maxima (column of S^T: lanes col, col+16,
+    // col+32, col+48): a row's maximum moves when the half exceeds it by more
+    // than kLazy (a row that has seen no key: on any visible key), scaling O
+    // and l by 2^-move.  Both stay runtime branches: a branch-free fast tile
+    // lets the scheduler hoist the second half's reads and products into
+    // the first half and spill.
+    auto half = [&](int kk) {
+      f32x4 sh[2][kSub];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-#pragma unroll
-      for (int s = 0; s < kSub; ++s) sacc[kt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < kKSteps; ++ks) {
+      for (int j = 0; j < 2; ++j) {
+        const int kt = 2 * kk + j;
         const int krow = 16 * kt + col;
-        const bf16x8 kop = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const u32x4*>(&cur.k[krow][8 * ((4 * ks + quad) ^ swz_k<D>(krow))]));
 #pragma unroll
-        for (int s = 0; s < kSub; ++s)
-          sacc[kt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[s][ks], sacc[kt][s], 0, 0, 0);
+        for (int ks = 0; ks < kKSteps; ++ks) {
+          const bf16x8 kop = __builtin_bit_cast(
+              bf16x8, *reinterpret_cast<const u32x4*>(&cur.k[krow][8 * ((4 * ks + quad) ^ swz_k<D>(krow))]));
+#pragma unroll
+          for (int s = 0; s < kSub; ++s)
+            sh[j][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[s][ks], ks == 0 ? neg_m[s] : sh[j][s], 0, 0, 0);
+        }
       }
-    }
-
-    // online softmax per row (column of S^T: lanes col, col+16, col+32, col+48),
-    // log2 domain.  The reference maximum m_run moves only when a tile's
-    // maximum exceeds it by more than kLazy, so most tiles skip rescaling
-    // O and l; p = 2^(t - m_run) then stays below 2^kLazy.  Masked scores
-    // become -inf in place (exp2 -> 0): no per-key branches, one shared
-    // softmax, and tiles wholly inside every row's range skip the mask.
-    bf16x8 pop[kSub][2];
-    {
+      if (masked) {
 #pragma unroll
-      for (int s = 0; s < kSub; ++s) {
-        f32x4 t[4];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) t[kt] = sacc[kt][s];
-        if (masked) {
+        for (int s = 0; s < kSub; ++s) {
           // causal: key index <= the row's token; window: key pos >= row pos - W
-          const int32_t climit = ext ? t0 + (row_th[s] & 0xffff) - base : kKeys;
+          const int r = row_of(s);
+          const int32_t climit = ext ? t0 + (r >> a.group_shift) - base : kKeys;
           const int32_t last = climit < count - 1 ? climit : count - 1;
-          const int32_t thr = a.window >= 0 ? row_rel[s] - a.window : -kFar - 1;
+          const int32_t thr = a.window >= 0 ? rel_rows[r] - a.window : -kFar - 1;
 #pragma unroll
-          for (int kt = 0; kt < 4; ++kt) {
-            const i32x4 kp = *reinterpret_cast<const i32x4*>(&cur.pos[16 * kt + 4 * quad]);
+          for (int j = 0; j < 2; ++j) {
+            const int k0 = 16 * (2 * kk + j) + 4 * quad;
+            const i32x4 kp = *reinterpret_cast<const i32x4*>(&cur.pos[k0]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const bool vis = (16 * kt + 4 * quad + i <= last) & (kp[i] >= thr);
-              t[kt][i] = vis ? t[kt][i] : -INFINITY;
+              const bool vis = (k0 + i <= last) & (kp[i] >= thr);
+              sh[j][s][i] = vis ? sh[j][s][i] : -INFINITY;
             }
           }
         }
-        // 16 values in 8 three-input maxima
-        const float m0 = max3(t[0][0], t[0][1], t[0][2]);
-        const float m1 = max3(t[0][3], t[1][0], t[1][1]);
-        const float m2 = max3(t[1][2], t[1][3], t[2][0]);
-        const float m3 = max3(t[2][1], t[2][2], t[2][3]);
-        const float m4 = max3(t[3][0], t[3][1], t[3][2]);
-        float mx = max3(max3(m0, m1, m2), max3(m3, m4, t[3][3]), -INFINITY);
-        mx = row_max(mx);
-        // mx = -inf when the row sees nothing here (never above bump_at)
-        const bool bump = mx > bump_at[s];
-        if (__builtin_amdgcn_ballot_w64(bump)) {
-          const float m_new = bump ? mx * a.scale_log2 : m_run[s];
-          const float alpha = bump ? __builtin_amdgcn_exp2f(m_run[s] - m_new) : 1.f;  // m_run = -inf -> 0
-          lacc[s] *= alpha;
+      }
+      if (exact) {
 #pragma unroll
-          for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] *= alpha;
-          m_run[s] = m_new;
-          // a row that has seen no key yet has only -inf scores: any finite shift
-          neg_m[s] = m_new == -INFINITY ? 0.f : -m_new;
-          bump_at[s] = (m_new + kLazy) / a.scale_log2;
-        }
+        for (int s = 0; s < kSub; ++s) {
+          // 8 values in 4 three-input maxima, then across the lane groups
+          const float m0 = max3(sh[0][s][0], sh[0][s][1], sh[0][s][2]);
+          const float m1 = max3(sh[0][s][3], sh[1][s][0], sh[1][s][1]);
+          float mx = max3(m0, m1, max3(sh[1][s][2], sh[1][s][3], -INFINITY));
+          mx = row_max(mx);  // -inf when the row sees nothing here
+          const bool seen = lacc[s][0] != 0.f;
+          const bool bump = seen ? mx > kLazy : mx > -INFINITY;
+          if (__builtin_amdgcn_ballot_w64(bump)) {
+            const float shift = bump ? mx : 0.f;
+            const float alpha = bump && seen ? __builtin_amdgcn_exp2f(-mx) : 1.f;
+            lacc[s] *= alpha;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          f32x4 e0, e1;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            e0[i] = __builtin_amdgcn_exp2f(fmaf(t[2 * kk][i], a.scale_log2, neg_m[s]));
-            e1[i] = __builtin_amdgcn_exp2f(fmaf(t[2 * kk + 1][i], a.scale_log2, neg_m[s]));
+            for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] *= alpha;
+            sh[0][s] -= shift;
+            sh[1][s] -= shift;
+            neg_m[s] -= shift;
           }
-          const bf16x4 b0 = __builtin_convertvector(e0, bf16x4);
-          const bf16x4 b1 = __builtin_convertvector(e1, bf16x4);
-          pop[s][kk] = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
         }
       }
-    }
-
-    // O^T += V^T . P^T
+      bf16x8 pop[kSub];
 #pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt)
+      for (int s = 0; s < kSub; ++s) {
+        f32x4 e0, e1;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
+        for (int i = 0; i < 4; ++i) {
+          e0[i] = __builtin_amdgcn_exp2f(sh[0][s][i]);
+          e1[i] = __builtin_amdgcn_exp2f(sh[1][s][i]);
+        }
+        const bf16x4 b0 = __builtin_convertvector(e0, bf16x4);
+        const bf16x4 b1 = __builtin_convertvector(e1, bf16x4);
+        pop[s] = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int s = 0; s < kSub; ++s) lacc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kOnes, pop[s], lacc[s], 0, 0, 0);
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) {
         // transposing read: lane col of group quad receives V[key][16dt + col]
         // for keys 32kk + 4 quad + i (i < 4), then 32kk + 16 + 4 quad + i;
         // source lane col supplies row key0 + col / 4, dims 16dt + 4 (col % 4) ..+3
@@ -468,22 +490,71 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
         const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int s = 0; s < kSub; ++s)
-          oacc[dt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[s][kk], oacc[dt][s], 0, 0, 0);
+          oacc[dt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[s], oacc[dt][s], 0, 0, 0);
       }
-    // row sums of the same bf16 weights on the matrix cores (a ones operand):
-    // the output stays a convex combination of the values
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int s = 0; s < kSub; ++s)
-        lacc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kOnes, pop[s][kk], lacc[s], 0, 0, 0);
+    };
+    half(0);
+    half(1);
 
+    // Without maxima the weights' sums are the check: a sum above kBig (a
+    // score ~26 above the maximum, or slow growth over many tiles) is
+    // renormalised by a power of two (exact); one above kHuge (a score ~58
+    // above the maximum, inf included) may have overflowed O: the workgroup
+    // restarts its keys with exact maxima on every tile.  NaN sums pass both
+    // tests: NaN inputs reach the output.
+    bool big = false, huge = false;
+#pragma unroll
+    for (int s = 0; s < kSub; ++s) {
+      big |= lacc[s][0] > kBig;
+      huge |= lacc[s][0] > kHuge;
+    }
+    if (__builtin_amdgcn_ballot_w64(big)) {
+      if (!exact && __builtin_amdgcn_ballot_w64(huge)) restart_flag = 1;
+      // sum -> [1/2, 1): O and the sum by 2^-e, the maximum up by e
+#pragma unroll
+      for (int s = 0; s < kSub; ++s) {
+        const int e = lacc[s][0] > kBig ? __builtin_amdgcn_frexp_expf(lacc[s][0]) : 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lacc[s][i] = __builtin_amdgcn_ldexpf(lacc[s][i], -e);
+#pragma unroll
+        for (int dt = 0; dt < kDTiles; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) oacc[dt][s][i] = __builtin_amdgcn_ldexpf(oacc[dt][s][i], -e);
+        neg_m[s] -= static_cast<float>(e);
+      }
+    }
+    if (unset) {
+      bool none = false;
+#pragma unroll
+      for (int s = 0; s < kSub; ++s) none |= lacc[s][0] == 0.f;
+      unset = __builtin_amdgcn_ballot_w64(none) != 0;
+    }
     if (it + 1 < n_tiles) commit(nxt);
     __syncthreads();
   };
+  // a restart (decided before the tile's barrier, read after it by every
+  // wave) starts the keys again from tile 0 with exact maxima; no load is in
+  // flight after a barrier and neither buffer is still being read
+  auto restart_flag_set = [&]() -> bool {
+    return !exact_all && __builtin_amdgcn_readfirstlane(*static_cast<volatile int32_t*>(&restart_flag));
+  };
+  auto restarted = [&]() -> bool {
+    if (!restart_flag_set()) return false;
+    exact_all = true;
+    unset = true;
+    clear_rows();
+    if (n_pref > 0) fetch_slots(0);
+    stage(0, tile0);
+    if (1 < n_pref) fetch_slots(1);
+    commit(tile0);
+    __syncthreads();
+    return true;
+  };
   for (int it = 0; it < n_tiles; it += 2) {
     step(it, tile0, tile1);
-    if (it + 1 < n_tiles) step(it + 1, tile1, tile0);
+    // a restart after the first half skips the second
+    if (it + 1 < n_tiles && !restart_flag_set()) step(it + 1, tile1, tile0);
+    if (restarted()) it = -2;
   }
 
   // normalise with the sink; store
@@ -492,13 +563,14 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
     float l = lacc[s][0];
     float scale = 1.f;
     if (a.sinks) {
-      const float sink = a.sinks[row_th[s] >> 16] * kLog2e;
-      const float m_f = fmaxf(m_run[s], sink);
-      scale = m_run[s] == -INFINITY ? 0.f : exp2f(m_run[s] - m_f);
+      const float m_run = l != 0.f ? -neg_m[s][0] : -INFINITY;
+      const float sink = a.sinks[g * G + (row_of(s) & (G - 1))] * kLog2e;
+      const float m_f = fmaxf(m_run, sink);
+      scale = m_run == -INFINITY ? 0.f : exp2f(m_run - m_f);
       l = l * scale + exp2f(sink - m_f);
     }
     const float inv = l > 0.f ? scale / l : 0.f;
-    const int32_t row_token = row_th[s] & 0xffff, row_head = row_th[s] >> 16;
+    const int32_t row_token = row_of(s) >> a.group_shift, row_head = g * G + (row_of(s) & (G - 1));
     if (t0 + row_token >= qlen) continue;
     const int64_t at =
         (qo0 + t0 + row_token) * a.o_st + static_cast<int64_t>(row_head) * a.o_sh + 4 * quad;
@@ -628,6 +700,7 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
   a.scale_log2 = scale * kLog2e;
   a.out_f32 = out_dtype == AKV_F32;
   a.group = q_heads / kv_heads;
+  while ((1 << a.group_shift) < a.group) ++a.group_shift;  // the group divides 128: a power of two
   a.tokens_per_block = rows_per_block(head_dim) / a.group;
   const int64_t blocks = (max_query_len + a.tokens_per_block - 1) / a.tokens_per_block;
   if (blocks * kv_heads > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_context_attention: queries too long");

@@ -179,6 +179,66 @@ def test_metadata_from_plain_requests(device):
     assert np.abs(_f32(out) - want).max() <= TOL
 
 
+LEVEL_PROFILES = {
+    # log2-domain score level of prefix tile t (64 keys) above tile 0
+    "ramp": lambda t: 25.0 * t,  # each tile 25 above the last: sums pass 2^32 every other tile
+    "jump40": lambda t: 40.0 * (t > 0),  # one tile's sum near 2^46: renormalised
+    "jump70": lambda t: 70.0 * (t > 0),  # near 2^76, past 2^64: the workgroup restarts exactly
+    "jump300": lambda t: 300.0 * (t > 0),  # 2^300 overflows to inf: restart
+    "drop": lambda t: -200.0 * (t > 0),  # later keys underflow to zero weight
+}
+
+
+@pytest.mark.parametrize("d,hq,hkv", [(64, 64, 8), (128, 32, 8)])
+@pytest.mark.parametrize("profile", sorted(LEVEL_PROFILES))
+@pytest.mark.parametrize("window", [-1, 100])
+def test_score_levels_across_tiles(device, d, hq, hkv, profile, window):
+    """Prefix keys whose scores sit far above (or below) the first tile's:
+    the running maximum comes from the first tile's exact row maxima, later
+    tiles skip the maxima, and their weight sums decide between keeping it,
+    renormalising by a power of two, and restarting the keys with exact
+    maxima.  Every case matches the float64 oracle, sinks included."""
+    scale = d ** -0.5
+    c = scale * 1.4426950408889634  # log2-domain scale
+    q_lens, p_lens, slots = [40, 200], [64 * 6, 64 * 3 + 10], 1200
+    g = torch.Generator().manual_seed(7 + d)
+    rng = np.random.default_rng(d)
+    nq = sum(q_lens)
+    q = torch.randn((nq, hq, d), generator=g) * 0.5
+    q[..., 0] = 8.0
+    ke = (torch.randn((nq, hkv, d), generator=g) * 0.5).to(torch.bfloat16)
+    ve = torch.randn((nq, hkv, d), generator=g).to(torch.bfloat16)
+    kp = torch.randn((slots, hkv, d), generator=g) * 0.5
+    vp = torch.randn((slots, hkv, d), generator=g).to(torch.bfloat16)
+    qo = np.concatenate(([0], np.cumsum(q_lens))).astype(np.int64)
+    kv = np.concatenate(([0], np.cumsum(p_lens))).astype(np.int64)
+    idx = (rng.permutation(slots - 1)[: kv[-1]] + 1).astype(np.int32)  # distinct slots
+    level = LEVEL_PROFILES[profile]
+    for s in range(len(p_lens)):
+        for j in range(p_lens[s]):
+            kp[idx[kv[s] + j], :, 0] = level(j // 64) / (c * 8.0)
+    q, kp = q.to(torch.bfloat16), kp.to(torch.bfloat16)
+    positions = window >= 0
+    kpos = np.concatenate([np.arange(p) * 2 for p in p_lens]).astype(np.int64)
+    qpos = np.concatenate([2 * p + np.arange(n) for n, p in zip(q_lens, p_lens)]).astype(np.int64)
+    sinks = torch.randn(hq, generator=torch.Generator().manual_seed(11)).to(device)
+    out = torch.full(q.shape, 7.0, dtype=torch.float32, device=device)
+    dq, dke, dve, dkp, dvp = (t.to(device) for t in (q, ke, ve, kp, vp))
+    print(f"score levels d={d} profile={profile} window={window}", flush=True)
+    ca.extend_attention_fwd(dq, dke, dve, out, dkp, dvp, torch.from_numpy(qo).to(device),
+                            torch.from_numpy(kv).to(device), torch.from_numpy(idx).to(device), None, True, None,
+                            max(q_lens), sm_scale=scale, sliding_window_size=window, sinks=sinks,
+                            context_q_positions=torch.from_numpy(qpos).to(device) if positions else None,
+                            context_kv_positions=torch.from_numpy(kpos).to(device) if positions else None)
+    torch.cuda.synchronize()
+    want = oat.context_attention(_f32(q), _f32(ke), _f32(ve), _f32(kp), _f32(vp), qo, kv, idx, scale,
+                                 window=window, q_positions=qpos if positions else None,
+                                 kv_positions=kpos if positions else None, sinks=_f32(sinks))
+    got = _f32(out)
+    assert np.isfinite(got).all()
+    assert np.abs(got - want).max() <= TOL
+
+
 def test_rejects_nonpositive_scale(device):
     """Masked scores are -inf before scaling, so the scale must be positive."""
     c = _case(device, 16, 2, 64, [5], [3], seed=4)
