@@ -71,7 +71,6 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 constexpr int sub_tiles(int d) { return d == 64 ? 4 : 2; }
 constexpr int rows_per_block(int d) { return 4 * 16 * sub_tiles(d); }  // (token, head) rows
 constexpr int kThreads = 256;
-constexpr int kKeys = 64;  // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.f;  // log2-domain slack before an exact maximum moves
 constexpr float kBig = 4294967296.f;  // 2^32: a weight sum above it is renormalised
@@ -144,11 +143,11 @@ __device__ __forceinline__ u32x4 load16b(const char* p) {
 // statically in each half of the unrolled tile loop, so the compiler sees
 // that this tile's LDS reads never touch the other buffer that the next
 // tile's direct loads are filling (no wait on those loads mid-tile).
-template <int D>
+template <int D, int KEYS>
 struct TileLds {
-  __bf16 k[kKeys][D];   // key-major K tile, 16 B chunks swizzled per row (swz_k)
-  __bf16 v[kKeys][D];   // key-major V tile, read transposed (ds_read_b64_tr_b16), swizzled (swz_v)
-  int32_t pos[kKeys];   // key positions relative to the block's first query
+  __bf16 k[KEYS][D];   // key-major K tile, 16 B chunks swizzled per row (swz_k)
+  __bf16 v[KEYS][D];   // key-major V tile, read transposed (ds_read_b64_tr_b16), swizzled (swz_v)
+  int32_t pos[KEYS];   // key positions relative to the block's first query
 };
 
 // Chunk swizzles: logical 16 B chunk c of row r lives at chunk c ^ swz(r).
@@ -171,13 +170,17 @@ __device__ __forceinline__ int32_t rel_pos(int64_t p, int64_t base) {
   return static_cast<int32_t>(r < -kFar ? -kFar : (r > kFar ? kFar : r));
 }
 
-template <int D, typename IdxT, typename PosT, bool POS>
+// KEYS keys per tile: 128 for full layers at head_dim 64 (half the tile
+// barriers, staging and commits per key), 64 for windowed layers (less of a
+// tile outside the window) and at head_dim 128 (LDS for two workgroups per CU)
+template <int D, int KEYS, typename IdxT, typename PosT, bool POS>
 __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const CtxArgs a) {
   constexpr int kSub = sub_tiles(D);
+  constexpr int kKeys = KEYS;
   constexpr int kChunks = D / 8;               // 16 B chunks per key row
   constexpr int kKSteps = D / 32;              // MFMA k-steps over head dims
   constexpr int kDTiles = D / 16;              // O^T row tiles
-  __shared__ __attribute__((aligned(16))) TileLds<D> tile0, tile1;
+  __shared__ __attribute__((aligned(16))) TileLds<D, KEYS> tile0, tile1;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -302,7 +305,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
       slot[u] = static_cast<uint32_t>(slots[j < plen ? j : plen - 1]);
     }
   };
-  auto stage = [&](int it, TileLds<D>& t) {
+  auto stage = [&](int it, TileLds<D, KEYS>& t) {
     // branch-free: keys past the end read the last valid row (masked out later)
     const bool ext = it >= n_pref;
     const int32_t base = tile_base(it);
@@ -336,7 +339,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   };
   // positions of the staged tile, then wait for its direct loads (vmcnt) so
   // the barrier that follows publishes the whole tile
-  auto commit = [&](TileLds<D>& t) {
+  auto commit = [&](TileLds<D, KEYS>& t) {
     if (tid < kKeys) t.pos[tid] = pvalid ? rel_pos(preg, qbase) : kFar;
     __builtin_amdgcn_s_waitcnt(0);
   };
@@ -373,7 +376,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   commit(tile0);
   __syncthreads();
   // tile it from cur while tile it + 1 streams into nxt
-  auto step = [&](int it, TileLds<D>& cur, TileLds<D>& nxt) {
+  auto step = [&](int it, TileLds<D, KEYS>& cur, TileLds<D, KEYS>& nxt) {
     if (it + 1 < n_tiles) {
       stage(it + 1, nxt);
       if (it + 2 < n_pref) fetch_slots(it + 2);
@@ -493,8 +496,14 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
           oacc[dt][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[s], oacc[dt][s], 0, 0, 0);
       }
     };
-    half(0);
-    half(1);
+    if constexpr (kKeys == 64) {
+      half(0);
+      half(1);
+    } else {
+      // rolled: unrolled, the four quarters' operand reads crowd the registers
+#pragma nounroll
+      for (int kk = 0; kk < kKeys / 32; ++kk) half(kk);
+    }
 
     // Without maxima the weights' sums are the check: a sum above kBig (a
     // score ~26 above the maximum, or slow growth over many tiles) is
@@ -589,30 +598,32 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   }
 }
 
-template <int D, typename IdxT>
+template <int D, int KEYS, typename IdxT>
 void launch_pos(int pos, dim3 grid, hipStream_t st, const CtxArgs& a) {
   // pos: 0 none, 1 int32, 2 int64
   if (pos == 2)
-    hipLaunchKernelGGL((context_attention_kernel<D, IdxT, int64_t, true>), grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((context_attention_kernel<D, KEYS, IdxT, int64_t, true>), grid, dim3(kThreads), 0, st, a);
   else if (pos == 1)
-    hipLaunchKernelGGL((context_attention_kernel<D, IdxT, int32_t, true>), grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((context_attention_kernel<D, KEYS, IdxT, int32_t, true>), grid, dim3(kThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((context_attention_kernel<D, IdxT, int64_t, false>), grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((context_attention_kernel<D, KEYS, IdxT, int64_t, false>), grid, dim3(kThreads), 0, st, a);
 }
 
-template <int D>
+template <int D, int KEYS>
 void launch_idx(bool idx64, int pos, dim3 grid, hipStream_t st, const CtxArgs& a) {
   if (idx64)
-    launch_pos<D, int64_t>(pos, grid, st, a);
+    launch_pos<D, KEYS, int64_t>(pos, grid, st, a);
   else
-    launch_pos<D, int32_t>(pos, grid, st, a);
+    launch_pos<D, KEYS, int32_t>(pos, grid, st, a);
 }
 
 void launch_typed(int head_dim, bool idx64, int pos, dim3 grid, hipStream_t st, const CtxArgs& a) {
-  if (head_dim == 64)
-    launch_idx<64>(idx64, pos, grid, st, a);
+  if (head_dim == 128)
+    launch_idx<128, 64>(idx64, pos, grid, st, a);
+  else if (a.window >= 0)
+    launch_idx<64, 64>(idx64, pos, grid, st, a);
   else
-    launch_idx<128>(idx64, pos, grid, st, a);
+    launch_idx<64, 128>(idx64, pos, grid, st, a);
 }
 
 }  // namespace
