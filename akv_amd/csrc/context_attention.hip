@@ -328,7 +328,8 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
       __builtin_amdgcn_global_load_lds(krow + 16 * ck, (lds_void*)(&t.k[blk * kRowsPerBlock][0]), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(vrow + 16 * cv, (lds_void*)(&t.v[blk * kRowsPerBlock][0]), 16, 0, 0);
     }
-    if (tid < kKeys) {
+    // key positions matter only to a window (causal masking is by index)
+    if (a.window >= 0 && tid < kKeys) {
       // loaded now, converted at commit: no wait on the tile's row loads here
       const int32_t j = base + tid;
       const int32_t end = ext ? e_hi : plen;
@@ -340,7 +341,8 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   // positions of the staged tile, then wait for its direct loads (vmcnt) so
   // the barrier that follows publishes the whole tile
   auto commit = [&](TileLds<D, KEYS>& t) {
-    if (tid < kKeys) t.pos[tid] = pvalid ? rel_pos(preg, qbase) : kFar;
+    // (without a window every key's position reads 0, which the mask admits)
+    if (tid < kKeys) t.pos[tid] = a.window < 0 ? 0 : (pvalid ? rel_pos(preg, qbase) : kFar);
     __builtin_amdgcn_s_waitcnt(0);
   };
 
@@ -387,9 +389,8 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
     const int count = left < kKeys ? left : kKeys;
     // masking is needed for a partial tile, keys past the block's first
     // query (causal), or keys older than the last query's window
-    const int32_t pos0 = __builtin_amdgcn_readfirstlane(cur.pos[0]);
     const bool masked = count < kKeys || (ext && base + kKeys - 1 > t0) ||
-                        (a.window >= 0 && pos0 < last_rel - a.window);
+                        (a.window >= 0 && __builtin_amdgcn_readfirstlane(cur.pos[0]) < last_rel - a.window);
     const bool exact = unset || exact_all;
 
     // The tile in two halves of 32 keys (kk), each complete before the next:
