@@ -22,24 +22,24 @@
 // G q heads of the group packed as rows: row r = token * G + head; R = 256
 // rows at head_dim 64 (4 waves x 64 rows, so each wave's reads of a K/V tile
 // from LDS feed 64 rows), 128 at head_dim 128 (4 waves x 32 rows).  Per
-// 64-key tile (K and V key-major in LDS with XOR-swizzled 16 B chunks,
-// double buffered; the next tile's rows stream straight from HBM into LDS
-// with global_load_lds_dwordx4 -- no staging registers -- and the slots of
-// the tile after it are fetched, all during this tile's math), for a wave's
-// W rows:
-//   S^T[64 keys x W rows] = K . Q^T - m       v_mfma_f32_16x16x32_bf16
+// tile of 128 keys (full layers at head_dim 64) or 64 (K and V key-major in
+// LDS with XOR-swizzled 16 B chunks, double buffered; the next tile's rows
+// stream straight from HBM into LDS with global_load_lds_dwordx4 -- no
+// staging registers -- and the slots of the tile after it are fetched, all
+// during this tile's math), in 32-key quarters, for a wave's W rows:
+//   S^T[32 keys x W rows] = K . Q^T - m       v_mfma_f32_16x16x32_bf16
 //     (Q carries the softmax scale in the log2 domain; the accumulator
 //     starts at each row's -m, so the scores leave the matrix cores ready
 //     for exp2)
 //   P^T = 2^(S^T) in bf16
-//   l[rows] = 1^T . P^T                       (row sums of the same bf16 P)
+//   l[rows] += 1^T . P^T                      (row sums of the same bf16 P)
 //   O^T[D x W rows] += V^T . P^T              v_mfma_f32_16x16x32_bf16
 // Online softmax without per-tile maxima: a row's running maximum m comes
-// from exact row maxima while the row has seen no key, then stays put; a
-// tile whose weight sum passes 2^32 (a score ~26 above m, or inf) is
-// computed again with exact maxima (moving m by the lazy rule: only when
-// the tile exceeds it by 2^8), and a running sum that passes 2^32 over many
-// tiles is renormalised by a power of two.
+// from exact row maxima (moving only when a quarter exceeds it by 2^8)
+// while some row of the wave has seen no key, then stays put.  After each
+// tile the weight sums are checked: one past 2^32 is renormalised by a power
+// of two; one past 2^64 (a score ~58 above m, or inf) may have overflowed O,
+// and the workgroup restarts its keys with exact maxima on every tile.
 // P^T leaves the first MFMA in the B-operand layout of the second (any
 // consistent split of the 32-long k axis over lanes gives the same product:
 // lane l uses keys 4(l/16)+i of two 16-key subtiles); V^T comes from the
