@@ -27,11 +27,10 @@
 // stream straight from HBM into LDS with global_load_lds_dwordx4 -- no
 // staging registers -- and the slots of the tile after it are fetched, all
 // during this tile's math), in 32-key quarters, for a wave's W rows:
-//   S^T[32 keys x W rows] = K . Q^T - m       v_mfma_f32_16x16x32_bf16
-//     (Q carries the softmax scale in the log2 domain; the accumulator
-//     starts at each row's -m, so the scores leave the matrix cores ready
-//     for exp2)
-//   P^T = 2^(S^T) in bf16
+//   S^T[32 keys x W rows] = K . Q^T           v_mfma_f32_16x16x32_bf16
+//   P^T = 2^(scale log2(e) S^T - m) in bf16   (one fp32 fma per score: Q
+//     stays exact -- folding the scale into a bf16 Q costs several times
+//     the tolerance once the scores spread over ~40 in the log2 domain)
 //   l[rows] += 1^T . P^T                      (row sums of the same bf16 P)
 //   O^T[D x W rows] += V^T . P^T              v_mfma_f32_16x16x32_bf16
 // Online softmax without per-tile maxima: a row's running maximum m comes
@@ -273,11 +272,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
       u32x4 w = {0u, 0u, 0u, 0u};
       if (ok)
         w = load16(a.q + (qo0 + t0 + tl) * a.q_st + static_cast<int64_t>(head) * a.q_sh + 32 * ks + 8 * quad);
-      // the softmax scale in the log2 domain is folded into Q (one bf16
-      // rounding), so the scores leave the matrix cores ready for exp2
-      const bf16x8 raw = __builtin_bit_cast(bf16x8, w);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qop[s][ks][i] = static_cast<__bf16>(static_cast<float>(raw[i]) * a.scale_log2);
+      qop[s][ks] = __builtin_bit_cast(bf16x8, w);
     }
   }
 
@@ -347,15 +342,15 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   };
 
   f32x4 oacc[kDTiles][kSub];
-  // per row: the negated running maximum -m (log2 domain) in all four
-  // entries of a quad that the score MFMAs accumulate onto, so the scores
-  // leave the matrix cores as t - m, and the running sum of the bf16 weights
-  // (4 equal copies); a row with a zero sum has seen no key (its quad holds 0)
-  f32x4 neg_m[kSub], lacc[kSub];
+  // per row: the negated running maximum -m (log2 domain; 0 while the row
+  // has seen no key) and the running sum of the bf16 weights (4 equal
+  // copies); a row with a zero sum has seen no key
+  float neg_m[kSub];
+  f32x4 lacc[kSub];
   auto clear_rows = [&]() {
 #pragma unroll
     for (int s = 0; s < kSub; ++s) {
-      neg_m[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+      neg_m[s] = 0.f;
       lacc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -393,10 +388,9 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
                         (a.window >= 0 && __builtin_amdgcn_readfirstlane(cur.pos[0]) < last_rel - a.window);
     const bool exact = unset || exact_all;
 
-    // The tile in two halves of 32 keys (kk), each complete before the next:
-    //   S^T = K . Q^T - m      (Q carries the scale: log2 domain; the first
-    //                           k-step accumulates onto -m)
-    //   P^T = 2^(S^T) in bf16  (the B operand of both products)
+    // The tile in quarters of 32 keys (kk), each complete before the next:
+    //   S^T = K . Q^T
+    //   P^T = 2^(scale log2(e) S^T - m) in bf16  (the B operand of both products)
     //   l += 1^T . P^T         (row sums of the same bf16 weights on the
     //                           matrix cores: O stays a convex combination)
     //   O^T += V^T . P^T
@@ -419,7 +413,8 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
               bf16x8, *reinterpret_cast<const u32x4*>(&cur.k[krow][8 * ((4 * ks + quad) ^ swz_k<D>(krow))]));
 #pragma unroll
           for (int s = 0; s < kSub; ++s)
-            sh[j][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[s][ks], ks == 0 ? neg_m[s] : sh[j][s], 0, 0, 0);
+            sh[j][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[s][ks],
+                                                               ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sh[j][s], 0, 0, 0);
         }
       }
       if (masked) {
@@ -450,17 +445,16 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
           const float m1 = max3(sh[0][s][3], sh[1][s][0], sh[1][s][1]);
           float mx = max3(m0, m1, max3(sh[1][s][2], sh[1][s][3], -INFINITY));
           mx = row_max(mx);  // -inf when the row sees nothing here
+          // the half's largest exponent, t - m in the log2 domain
+          const float top = fmaf(mx, a.scale_log2, neg_m[s]);
           const bool seen = lacc[s][0] != 0.f;
-          const bool bump = seen ? mx > kLazy : mx > -INFINITY;
+          const bool bump = seen ? top > kLazy : mx > -INFINITY;
           if (__builtin_amdgcn_ballot_w64(bump)) {
-            const float shift = bump ? mx : 0.f;
-            const float alpha = bump && seen ? __builtin_amdgcn_exp2f(-mx) : 1.f;
+            const float alpha = bump && seen ? __builtin_amdgcn_exp2f(-top) : 1.f;
             lacc[s] *= alpha;
 #pragma unroll
             for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] *= alpha;
-            sh[0][s] -= shift;
-            sh[1][s] -= shift;
-            neg_m[s] -= shift;
+            neg_m[s] = bump ? -(mx * a.scale_log2) : neg_m[s];
           }
         }
       }
@@ -470,8 +464,8 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
         f32x4 e0, e1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          e0[i] = __builtin_amdgcn_exp2f(sh[0][s][i]);
-          e1[i] = __builtin_amdgcn_exp2f(sh[1][s][i]);
+          e0[i] = __builtin_amdgcn_exp2f(fmaf(sh[0][s][i], a.scale_log2, neg_m[s]));
+          e1[i] = __builtin_amdgcn_exp2f(fmaf(sh[1][s][i], a.scale_log2, neg_m[s]));
         }
         const bf16x4 b0 = __builtin_convertvector(e0, bf16x4);
         const bf16x4 b1 = __builtin_convertvector(e1, bf16x4);
@@ -573,7 +567,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
     float l = lacc[s][0];
     float scale = 1.f;
     if (a.sinks) {
-      const float m_run = l != 0.f ? -neg_m[s][0] : -INFINITY;
+      const float m_run = l != 0.f ? -neg_m[s] : -INFINITY;
       const float sink = a.sinks[g * G + (row_of(s) & (G - 1))] * kLog2e;
       const float m_f = fmaxf(m_run, sink);
       scale = m_run == -INFINITY ? 0.f : exp2f(m_run - m_f);

@@ -239,6 +239,62 @@ def test_score_levels_across_tiles(device, d, hq, hkv, profile, window):
     assert np.abs(got - want).max() <= TOL
 
 
+@pytest.mark.parametrize("mag", [1.0, 3.0])
+@pytest.mark.parametrize("seed", range(10))
+def test_random_layouts(device, seed, mag):
+    """Seeded random batches: 1-4 segments of 1-299 queries over 0-699
+    prefix keys, head_dim 64 or 128, 1-8 KV heads, groups of 1-16, windows
+    none / 0 / 7 / 64 / 200 with and without positions, with and without
+    sinks; Q and K scaled by ``mag`` (3 puts the scores' spread near 40 in
+    the log2 domain, where a bf16 rounding of the scaled Q would already
+    cost several times the tolerance)."""
+    rng = np.random.default_rng(1000 + seed)
+    d = [64, 128][seed % 2]
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    hq = hkv * int(rng.choice([1, 2, 4, 8, 16]))
+    n_seg = int(rng.integers(1, 5))
+    q_lens = rng.integers(1, 300, n_seg)
+    p_lens = rng.integers(0, 700, n_seg)
+    window = int(rng.choice([-1, -1, 0, 7, 64, 200]))
+    positions = bool(rng.random() < 0.5)
+    with_sinks = bool(rng.random() < 0.5)
+    slots = int(p_lens.sum()) + 16
+    g = torch.Generator().manual_seed(seed)
+    nq = int(q_lens.sum())
+    q = (torch.randn((nq, hq, d), generator=g) * mag).to(torch.bfloat16)
+    ke = (torch.randn((nq, hkv, d), generator=g) * mag).to(torch.bfloat16)
+    ve = torch.randn((nq, hkv, d), generator=g).to(torch.bfloat16)
+    kp = (torch.randn((slots, hkv, d), generator=g) * mag).to(torch.bfloat16)
+    vp = torch.randn((slots, hkv, d), generator=g).to(torch.bfloat16)
+    qo = np.concatenate(([0], np.cumsum(q_lens))).astype(np.int64)
+    kv = np.concatenate(([0], np.cumsum(p_lens))).astype(np.int64)
+    idx = (rng.permutation(slots - 1)[: kv[-1]] + 1).astype(np.int32)
+    kpos, qpos = [], []
+    for n, p in zip(q_lens, p_lens):
+        allp = np.sort(rng.choice(3 * (n + p) + 8, size=n + p, replace=False))
+        kpos.append(allp[:p])
+        qpos.append(allp[p:])
+    kpos = np.concatenate(kpos).astype(np.int64)
+    qpos = np.concatenate(qpos).astype(np.int64)
+    sinks = (torch.randn(hq, generator=g) * 2).to(device) if with_sinks else None
+    scale = d ** -0.5
+    print(f"random layout seed={seed} mag={mag} d={d} hq={hq} hkv={hkv} segments={n_seg} window={window} "
+          f"positions={positions} sinks={with_sinks}", flush=True)
+    out = torch.full(q.shape, 7.0, dtype=torch.float32, device=device)
+    ca.extend_attention_fwd(q.to(device), ke.to(device), ve.to(device), out, kp.to(device), vp.to(device),
+                            torch.from_numpy(qo).to(device), torch.from_numpy(kv).to(device),
+                            torch.from_numpy(idx).to(device), None, True, None, int(q_lens.max()),
+                            sm_scale=scale, sliding_window_size=window, sinks=sinks,
+                            context_q_positions=torch.from_numpy(qpos).to(device) if positions else None,
+                            context_kv_positions=torch.from_numpy(kpos).to(device) if positions else None)
+    torch.cuda.synchronize()
+    want = oat.context_attention(_f32(q), _f32(ke), _f32(ve), _f32(kp), _f32(vp), qo, kv, idx, scale,
+                                 window=window, q_positions=qpos if positions else None,
+                                 kv_positions=kpos if positions else None,
+                                 sinks=_f32(sinks) if sinks is not None else None)
+    assert np.abs(_f32(out) - want).max() <= TOL
+
+
 def test_rejects_nonpositive_scale(device):
     """Masked scores are -inf before scaling, so the scale must be positive."""
     c = _case(device, 16, 2, 64, [5], [3], seed=4)
