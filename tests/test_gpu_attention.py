@@ -24,16 +24,18 @@ def _f32(t):
 
 @pytest.mark.parametrize("head_dim", [64, 128])
 @pytest.mark.parametrize("with_sinks", [True, False])
-def test_random_lengths_match_oracle(device, head_dim, with_sinks):
+# mag scales Q and K: 3 spreads the scores over ~40 in the log2 domain
+@pytest.mark.parametrize("mag", [1.0, 3.0])
+def test_random_lengths_match_oracle(device, head_dim, with_sinks, mag):
     g = torch.Generator().manual_seed(head_dim + with_sinks)
     rng = np.random.default_rng(head_dim)
     slots, hq, hkv = 20000, 64, 8
-    k = torch.randn((slots, hkv, head_dim), generator=g).to(torch.bfloat16).to(device)
+    k = (torch.randn((slots, hkv, head_dim), generator=g) * mag).to(torch.bfloat16).to(device)
     v = torch.randn((slots, hkv, head_dim), generator=g).to(torch.bfloat16).to(device)
     lengths = [0, 1, 15, 16, 17, 255, 256, 257, 1000, 5000]
     indptr = np.concatenate(([0], np.cumsum(lengths))).astype(np.int32)
     idx = rng.integers(1, slots, size=indptr[-1]).astype(np.int32)
-    q = torch.randn((len(lengths), hq, head_dim), generator=g).to(torch.bfloat16).to(device)
+    q = (torch.randn((len(lengths), hq, head_dim), generator=g) * mag).to(torch.bfloat16).to(device)
     sinks = (torch.randn(hq, generator=g) * 2).to(device) if with_sinks else None
     scale = head_dim ** -0.5
     for out_dtype in (torch.bfloat16, torch.float32):
