@@ -14,7 +14,9 @@
 // softmax per head (column), then O^T[D x 16] += V^T[D x 16] . P^T[16 x 16]
 // where P^T is already in the B-operand layout of the second MFMA (no
 // shuffle) and V goes through LDS to be read transposed.  A combine kernel
-// merges the chunks and the sink.
+// merges the chunks and the sink; when every request fits one chunk (a
+// sliding-window layer) the partial kernel applies the sink itself and the
+// combine is not launched.
 //
 // MFMA 16x16x16 bf16 lane layout (verified on gfx950): lane l supplies
 // A[l%16][4(l/16)+i] and B[4(l/16)+i][l%16] and holds D[4(l/16)+i][l%16].
@@ -77,6 +79,24 @@ __global__ void __launch_bounds__(64) decode_attention_partial_kernel(const Attn
   const int col = lane & 15;   // head within the group (B / D layout column)
   const int quad = lane >> 4;  // 0..3
   if (c0 >= len) {
+    if (a.chunks == 1) {
+      // one chunk and no keys: the output is 0, sink or not (no combine runs)
+      if (col < a.group) {
+        const int64_t at = static_cast<int64_t>(b) * a.out_stride_b +
+                           static_cast<int64_t>(g * a.group + col) * a.out_stride_h;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int d = 16 * t + 4 * quad + i;
+            if (a.out_f32)
+              static_cast<float*>(a.out)[at + d] = 0.f;
+            else
+              static_cast<__bf16*>(a.out)[at + d] = static_cast<__bf16>(0.f);
+          }
+      }
+      return;
+    }
     // empty chunk: neutral partial (m = -inf, l = 0)
     if (quad == 0) {
       part[col * (D + 2) + D] = -INFINITY;
@@ -203,6 +223,33 @@ __global__ void __launch_bounds__(64) decode_attention_partial_kernel(const Attn
   }
   // lane holds O^T[dims 16t + 4*quad + i][head col]; every lane of a column
   // carries that head's m and l
+  if (a.chunks == 1) {
+    // one chunk holds every key: normalise with the sink here (the combine's
+    // arithmetic for a single partial) and skip the combine launch
+    if (col < a.group) {
+      const int h = g * a.group + col;
+      const float sink = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
+      const bool valid = m_run != -INFINITY;
+      const float mt = valid ? fmaxf(sink, m_run) : sink;
+      float lt = (a.sinks && mt != -INFINITY) ? exp2f(sink - mt) : 0.f;
+      const float sw = valid ? exp2f(m_run - mt) : 0.f;
+      lt += valid ? l_run * sw : 0.f;
+      const int64_t at = static_cast<int64_t>(b) * a.out_stride_b + static_cast<int64_t>(h) * a.out_stride_h;
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float ot = valid ? acc[t][i] * sw : 0.f;
+          const float r = lt > 0.f ? ot / lt : 0.f;
+          const int d = 16 * t + 4 * quad + i;
+          if (a.out_f32)
+            static_cast<float*>(a.out)[at + d] = r;
+          else
+            static_cast<__bf16*>(a.out)[at + d] = static_cast<__bf16>(r);
+        }
+    }
+    return;
+  }
   if (col < a.group) {
     float* ph = part + col * (D + 2);
 #pragma unroll
@@ -385,13 +432,13 @@ extern "C" int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q
   if (head_dim == 64) {
     hipLaunchKernelGGL(decode_attention_partial_kernel<64>, grid, block, 0, st, a);
     int rc = check_launch("akv_decode_attention (partial)");
-    if (rc) return rc;
+    if (rc || a.chunks == 1) return rc;
     hipLaunchKernelGGL(decode_attention_combine_kernel<64>, dim3(n_requests, q_heads), dim3(kWays * 64), 0, st,
                        a);
   } else {
     hipLaunchKernelGGL(decode_attention_partial_kernel<128>, grid, block, 0, st, a);
     int rc = check_launch("akv_decode_attention (partial)");
-    if (rc) return rc;
+    if (rc || a.chunks == 1) return rc;
     hipLaunchKernelGGL(decode_attention_combine_kernel<128>, dim3(n_requests, q_heads), dim3(kWays * 128), 0,
                        st, a);
   }

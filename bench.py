@@ -370,7 +370,8 @@ def decode_consumer_config(device, flush):
         "full_layer_ms": round(warm_full, 5), "full_layer_p50_ms": round(percentile(cold_full, 50), 5),
         "full_layer_kv_GBs": round(kv_bytes / (warm_full / 1e3) / 1e9, 1),
         "window128_layer_ms": round(warm_win, 5), "window128_layer_p50_ms": round(percentile(cold_win, 50), 5),
-        "kernel_launches_per_layer": 2,
+        # split over key chunks + combine; a window layer's keys fit one chunk
+        "kernel_launches_per_layer": {"full": 2, "window128": 1},
         "metadata": {
             "full_ms": round(warm_meta_full, 5), "full_p50_ms": round(percentile(cold_meta_full, 50), 5),
             "full_p99_ms": round(percentile(cold_meta_full, 99), 5),

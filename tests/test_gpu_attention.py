@@ -26,13 +26,16 @@ def _f32(t):
 @pytest.mark.parametrize("with_sinks", [True, False])
 # mag scales Q and K: 3 spreads the scores over ~40 in the log2 domain
 @pytest.mark.parametrize("mag", [1.0, 3.0])
-def test_random_lengths_match_oracle(device, head_dim, with_sinks, mag):
+# long: split over key chunks, merged by the combine; short (at most one
+# 256-key chunk): normalised by the one launch
+@pytest.mark.parametrize("lengths", [[0, 1, 15, 16, 17, 255, 256, 257, 1000, 5000],
+                                     [0, 1, 15, 16, 17, 100, 129, 255, 256]], ids=["long", "short"])
+def test_random_lengths_match_oracle(device, head_dim, with_sinks, mag, lengths):
     g = torch.Generator().manual_seed(head_dim + with_sinks)
     rng = np.random.default_rng(head_dim)
     slots, hq, hkv = 20000, 64, 8
     k = (torch.randn((slots, hkv, head_dim), generator=g) * mag).to(torch.bfloat16).to(device)
     v = torch.randn((slots, hkv, head_dim), generator=g).to(torch.bfloat16).to(device)
-    lengths = [0, 1, 15, 16, 17, 255, 256, 257, 1000, 5000]
     indptr = np.concatenate(([0], np.cumsum(lengths))).astype(np.int32)
     idx = rng.integers(1, slots, size=indptr[-1]).astype(np.int32)
     q = (torch.randn((len(lengths), hq, head_dim), generator=g) * mag).to(torch.bfloat16).to(device)
