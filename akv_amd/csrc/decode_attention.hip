@@ -31,6 +31,7 @@ namespace {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) u32x4 global_u32x4;
 
@@ -264,49 +265,58 @@ __global__ void __launch_bounds__(64) decode_attention_partial_kernel(const Attn
 }
 
 // One workgroup per (request, q head): merge chunk partials and the sink.
-// kWays groups of D threads each fold every kWays-th chunk with an online
+// kCombineThreads threads in ways of D / 4 lanes (four dims per lane: two
+// 8-byte loads per chunk, as a partial row of D + 2 floats is 8-byte
+// aligned); each way folds every ways-th chunk with an online
 // (max, sum) merge -- the loads of one chunk do not wait on the previous
-// one -- and the groups meet in LDS.
-constexpr int kWays = 4;
+// one -- and the ways meet in LDS.
+constexpr int kCombineThreads = 256;
 
 template <int D>
-__global__ void __launch_bounds__(kWays * D) decode_attention_combine_kernel(const AttnArgs a) {
+__global__ void __launch_bounds__(kCombineThreads) decode_attention_combine_kernel(const AttnArgs a) {
+  constexpr int kLanes = D / 4;
+  constexpr int kWays = kCombineThreads / kLanes;
   __shared__ float s_m[kWays], s_l[kWays];
-  __shared__ float s_o[kWays][D];
+  __shared__ __attribute__((aligned(16))) float s_o[kWays][D];
   const int b = blockIdx.x;
   const int h = blockIdx.y;
   const int g = h / a.group;
   const int hl = h - g * a.group;
-  const int d = threadIdx.x % D;
-  const int way = threadIdx.x / D;
+  const int dl = threadIdx.x % kLanes;
+  const int way = threadIdx.x / kLanes;
   const int64_t len = a.kv_indptr[b + 1] - a.kv_indptr[b];
   // keys past max_len (a caller error) are not read: the partials stop there
   const int64_t want = (len + kChunk - 1) / kChunk;
   const int used = static_cast<int>(want < a.chunks ? want : a.chunks);
   const float* base = a.partial + (static_cast<int64_t>(b) * a.kv_heads + g) * a.chunks * 16 * (D + 2);
-  float m = -INFINITY, l = 0.f, o = 0.f;
-#pragma unroll 4
+  float m = -INFINITY, l = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
   for (int c = way; c < used; c += kWays) {
     const float* pc = base + (c * 16 + hl) * (D + 2);
     const float mc = pc[D];
     const float lc = pc[D + 1];
-    const float oc = pc[d];
+    // a partial row is D + 2 floats: 8-byte aligned, so two 8-byte loads
+    const f32x2_t lo = *reinterpret_cast<const f32x2_t*>(pc + 4 * dl);
+    const f32x2_t hi = *reinterpret_cast<const f32x2_t*>(pc + 4 * dl + 2);
+    const f32x4 oc = {lo.x, lo.y, hi.x, hi.y};
     // an empty chunk carries m = -inf and no o values
     const bool valid = mc != -INFINITY;
     const float mn = valid ? fmaxf(m, mc) : m;
     const float ws = valid ? exp2f(m - mn) : 1.f;
     const float wc = valid ? exp2f(mc - mn) : 0.f;
     l = l * ws + (valid ? lc : 0.f) * wc;
-    o = o * ws + (valid ? oc : 0.f) * wc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = o[i] * ws + (valid ? oc[i] : 0.f) * wc;
     m = mn;
   }
-  s_o[way][d] = o;
-  if (d == 0) {
+  *reinterpret_cast<f32x4*>(&s_o[way][4 * dl]) = o;
+  if (dl == 0) {
     s_m[way] = m;
     s_l[way] = l;
   }
   __syncthreads();
-  if (way != 0) return;
+  if (threadIdx.x >= D) return;
+  const int d = threadIdx.x;
   float mt = a.sinks ? a.sinks[h] * kLog2e : -INFINITY;
 #pragma unroll
   for (int w = 0; w < kWays; ++w) mt = fmaxf(mt, s_m[w]);
@@ -433,13 +443,13 @@ extern "C" int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q
     hipLaunchKernelGGL(decode_attention_partial_kernel<64>, grid, block, 0, st, a);
     int rc = check_launch("akv_decode_attention (partial)");
     if (rc || a.chunks == 1) return rc;
-    hipLaunchKernelGGL(decode_attention_combine_kernel<64>, dim3(n_requests, q_heads), dim3(kWays * 64), 0, st,
-                       a);
+    hipLaunchKernelGGL(decode_attention_combine_kernel<64>, dim3(n_requests, q_heads), dim3(kCombineThreads), 0,
+                       st, a);
   } else {
     hipLaunchKernelGGL(decode_attention_partial_kernel<128>, grid, block, 0, st, a);
     int rc = check_launch("akv_decode_attention (partial)");
     if (rc || a.chunks == 1) return rc;
-    hipLaunchKernelGGL(decode_attention_combine_kernel<128>, dim3(n_requests, q_heads), dim3(kWays * 128), 0,
+    hipLaunchKernelGGL(decode_attention_combine_kernel<128>, dim3(n_requests, q_heads), dim3(kCombineThreads), 0,
                        st, a);
   }
   return check_launch("akv_decode_attention (combine)");
