@@ -240,6 +240,40 @@ def test_every_tile_size(device, n_requests, want):
     _run(device, w, generated=[1] * w.n_requests)
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_batches(device, seed):
+    """Seeded random batches: 1-512 requests (one- and two-launch paths,
+    every tile size the total picks), up to ~1.5 M tokens, 0-3 drop spans
+    and 0-3 generated tokens per request, side rows or the table; every
+    output bit-exact against the oracle."""
+    rng = np.random.default_rng(5000 + seed)
+    n_requests = int(rng.choice([1, 2, 7, 64, 300, 512]))
+    total = int(rng.integers(max(n_requests, 1000), 1_500_000))
+    cuts = np.sort(rng.choice(np.arange(1, total), size=n_requests - 1, replace=False))
+    lengths = np.diff(np.concatenate(([0], cuts, [total])))
+    spans = []
+    for n in lengths:
+        n = int(n)
+        k = int(rng.integers(0, 4)) if n > 8 else 0
+        starts = np.sort(rng.choice(np.arange(n - 1), size=k, replace=False)) if k else []
+        req, prev = [], 0
+        for a in starts:
+            a = max(int(a), prev + 1 if req else 0)  # ordered, disjoint, not touching
+            b = min(n, a + 1 + int(rng.integers(0, max(1, n // 4))))
+            if a < b:
+                req.append((a, b))
+                prev = b
+        spans.append(tuple(req))
+    w = synth.Workload(f"random-{seed}", synth.TINY, tuple(int(n) for n in lengths), tuple(spans), seed=seed,
+                       table_positions=int(lengths.max()) + 8, pool_slots=3 * total + 1)
+    generated = [int(g) for g in rng.integers(0, 4, n_requests)]
+    side_rows = bool(rng.random() < 0.3)
+    lib = _lib.load()
+    print(f"random batch seed={seed}: {n_requests} requests, {total} tokens, path {_path(lib, n_requests, total)}, "
+          f"side rows {side_rows}", flush=True)
+    _run(device, w, generated=generated, side_rows=side_rows)
+
+
 def test_prefix_over_many_tiles(device):
     # 80 x 64k tokens (two-launch path): 5000+ tiles of 1024 tokens, each
     # summing the aggregates of up to 5000 earlier tiles
