@@ -94,7 +94,7 @@ def place_spans(rng, n, lengths):
     """Seeded composition of the kept tokens into ``k + 1`` gaps (interior >= 1)."""
     k = len(lengths)
     kept = n - int(np.sum(lengths))
-    free = kept - (k - 1)
+    free = kept - max(k - 1, 0)
     if free < 0:
         raise ValueError("spans do not fit")
     # stars and bars: k cut positions among free + k slots

@@ -276,7 +276,7 @@ def _paged_counts(keep, birth, final, page_size):
     copy_from = p0 * page_size
     # pages below p0 stay in place, unrotated: their tokens must already sit
     # at their final positions
-    if not np.array_equal(birth[:copy_from], np.arange(copy_from)):
+    if not np.array_equal(birth[:copy_from], np.arange(min(n, copy_from))):
         raise ValueError("paged compaction keeps the pages before the first drop in place: their tokens' "
                          "birth positions must equal their ranks")
     copies = max(0, kept - copy_from)
@@ -391,17 +391,31 @@ def compact_pages(inputs, req_to_token, req_rows, fresh_pages, outputs, *, row_p
         raise ValueError("row_pointers must be int64 addresses")
     if row_pointers is None and req_to_token.shape[1] < inputs.max_tokens:
         raise ValueError("req_to_token rows are shorter than the longest request")
+    sizes = dict(copy_src=(sum(inputs.copies),), copy_dst=(sum(inputs.copies),), copy_pairs=(sum(inputs.copies), 2),
+                 released_pages=(sum(inputs.released_pages),), page_table=(sum(inputs.new_pages),),
+                 raw_indices=(sum(inputs.kept),), active_positions=(sum(inputs.kept),))
+    for name, shape in sizes.items():
+        t = getattr(outputs, name)
+        if t.dtype != torch.int32 or tuple(t.shape) != shape or not t.is_contiguous():
+            raise ValueError(f"outputs.{name} must be a contiguous int32 tensor of shape {shape}")
     lib = _lib.load()
     device = req_to_token.device
+    # an empty list (a batch with nothing copied or released) gets a valid
+    # one-element stand-in: the kernel's writes to it are bounded by a zero total
+    spare = torch.empty(2, dtype=torch.int32, device=device)
+
+    def out(name):
+        t = getattr(outputs, name)
+        return t.data_ptr() if t.numel() else spare.data_ptr()
+
     with _on_device(device):
         rc = lib.akv_compact_pages(
             inputs.n_requests, inputs.req_offsets.data_ptr(), inputs.max_tokens, inputs.page_size,
             req_to_token.data_ptr(), req_to_token.stride(0), _lib.ptr(row_pointers), req_rows.data_ptr(),
             inputs.keep.data_ptr(), inputs.birth_positions.data_ptr(), inputs.final_positions.data_ptr(),
             _lib.ptr(birth_slots), inputs.bases.data_ptr(), _lib.ptr(fresh_pages) if fresh_pages.numel() else None,
-            outputs.copy_src.data_ptr(), outputs.copy_dst.data_ptr(), outputs.copy_pairs.data_ptr(),
-            outputs.released_pages.data_ptr(), outputs.page_table.data_ptr(), outputs.raw_indices.data_ptr(),
-            outputs.active_positions.data_ptr(), current_stream_handle(device),
+            out("copy_src"), out("copy_dst"), out("copy_pairs"), out("released_pages"), out("page_table"),
+            out("raw_indices"), out("active_positions"), current_stream_handle(device),
         )
     _lib.check(rc, "akv_compact_pages")
     return outputs

@@ -200,3 +200,58 @@ def test_page_one_matches_compact_rows(device):
     assert torch.equal(out.raw_indices, pout.raw_indices)
     assert torch.equal(out.active_positions, pout.active_positions)
     assert n == t1.shape[1]
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_shared_prefix(device, seed):
+    # seeded random batches: page size, prefix, suffixes, drop counts and
+    # lengths, and the grouping of requests all vary; a small 2-layer pool
+    # checks every copy (K against the oracle's rotation, V bit for bit)
+    rng = np.random.default_rng(500 + seed)
+    P = int(rng.choice([2, 4, 16, 32, 64]))
+    B = int(rng.integers(1, 25))
+    prefix = P * int(rng.integers(1, max(2, 640 // P)))
+    k_hi = int(rng.integers(0, 7))
+    k_lo = int(rng.integers(0, k_hi + 1))
+    span_hi = max(1, min(40, (prefix - k_hi) // max(k_hi, 1) - 1))
+    suffix_hi = int(rng.integers(0, 200))
+    w = synth.shared_prefix_workload(f"paged-random-{seed}", synth.TINY, B, prefix, 0, suffix_hi, k_lo, k_hi,
+                                     1, span_hi, P, seed=seed)
+    if rng.random() < 0.5:
+        split = None
+    else:
+        perm = rng.permutation(B)
+        cuts = np.sort(rng.choice(np.arange(1, B), size=min(B - 1, int(rng.integers(0, 4))), replace=False))
+        split = [list(g) for g in np.split(perm, cuts)]
+    a = synth.assign_pages(w, split)
+    layouts = synth.compile_layouts(w)
+    print(f"paged random {seed}: P={P} B={B} prefix={prefix} groups={len(a.groups)} pages={a.pool_pages}",
+          flush=True)
+    pool = synth.make_pool(w.model, a.pool_pages * P, device, seed=seed)
+    cos_sin = synth.rope_table(w, device)
+    k_before = [t.clone() for t in pool.k]
+    v_before = [t.clone() for t in pool.v]
+    order = rng.permutation(B + 3)[:B]
+    table = _table_for(a.birth_rows, max(w.lengths) + 5, device, order)
+    got = _run_groups(w, a, layouts, table, order, device, pool, cos_sin)
+    torch.cuda.synchronize()
+    _check_tables(w, a, layouts, got, table, order)
+
+    src = np.concatenate([got[b]["copy_source_slots"] for b in range(B)]).astype(np.int64)
+    dst = np.concatenate([got[b]["copy_destination_slots"] for b in range(B)]).astype(np.int64)
+    pairs = np.concatenate([got[b]["copy_position_pairs"] for b in range(B)]).reshape(-1, 2)
+    assert len(np.unique(dst)) == len(dst)
+    untouched = np.ones(a.pool_pages * P, dtype=bool)
+    untouched[dst] = False
+    table_np = to_storage(cos_sin)
+    for l in range(w.model.n_layers):
+        k0, v0 = to_storage(k_before[l]), to_storage(v_before[l])
+        k1, v1 = to_storage(pool.k[l]), to_storage(pool.v[l])
+        np.testing.assert_array_equal(v1[dst], v0[src], err_msg=f"V of layer {l}")
+        np.testing.assert_array_equal(k1[untouched], k0[untouched], err_msg=f"K of layer {l}")
+        np.testing.assert_array_equal(v1[untouched], v0[untouched], err_msg=f"V of layer {l}")
+        m = len(src)
+        kk = [np.concatenate((k0[src], np.zeros((m,) + k0.shape[1:], np.uint16)))]
+        vv = [np.zeros_like(kk[0])]
+        rp.reposition_kv_layers(kk, vv, np.arange(m), np.arange(m, 2 * m), pairs, table_np, dtype="bf16")
+        assert storage_equal(k1[dst], kk[0][m:]), f"K of layer {l}"

@@ -124,3 +124,20 @@ def test_pack_paged_inputs_rejects_prefix_births_off_rank():
     late = birth.copy()
     late[50] = 52
     tables.pack_paged_inputs([SimpleNamespace(keep_mask=keep, positions=final, birth_positions=late)], P, "cpu")
+
+
+@pytest.mark.parametrize("n", [37, 48])
+def test_pack_paged_inputs_undropped_request(n):
+    # nothing dropped: p0 lies past the last page, so p0 * P may exceed a
+    # ragged length; nothing is copied, released or handed out
+    P = 16
+    keep = np.ones(n, dtype=bool)
+    pos = np.arange(n, dtype=np.int32)
+    from types import SimpleNamespace
+
+    inp = tables.pack_paged_inputs([SimpleNamespace(keep_mask=keep, positions=pos, birth_positions=pos)], P, "cpu")
+    bases = inp.bases.numpy()
+    assert bases[0, 0] == -(-n // P) * P
+    assert bases[2, 1] == bases[3, 1] == bases[5, 1] == 0
+    assert bases[4, 1] == -(-n // P)
+    assert inp.fresh_pages == (0,)
