@@ -164,6 +164,9 @@ int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets,
  *   row 0: p0 * P per request; rows 1..5: exclusive offsets of kept
  *   tokens, copies, fresh pages, page-table entries and released pages.
  * One launch, one thread per raw token; every write is bounded by bases.
+ * Every list pointer must be non-null, also for a list whose total in bases
+ * is 0 (a batch with nothing copied or released): nothing is written
+ * through it then, so any valid device word will do.
  * No counterpart in the reference, whose Reposition rejects page_size != 1
  * (akv/system/sglang/kernels/ops/attention/context_reposition.py:153-154);
  * its P = 1 case equals akv_compact_rows' row/copy outputs
