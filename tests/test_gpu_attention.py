@@ -56,6 +56,46 @@ def test_random_lengths_match_oracle(device, head_dim, with_sinks, mag, lengths)
             assert err <= TOL, f"request {b} (len {n}) max err {err}"
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_batches_match_oracle(device, seed):
+    # seeded random batches: batch size, KV heads, GQA group (1-16), head
+    # dim, ragged lengths (empty, inside one chunk, over many), a host bound
+    # above the longest request (empty trailing chunks), sinks, spread and
+    # output dtype all vary
+    rng = np.random.default_rng(700 + seed)
+    g = torch.Generator().manual_seed(700 + seed)
+    head_dim = int(rng.choice([64, 128]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    hq = hkv * int(rng.choice([1, 2, 4, 8, 16]))
+    B = int(rng.integers(1, 41))
+    kind = rng.integers(0, 3, size=B)
+    lengths = np.where(kind == 0, rng.integers(0, 3, size=B),
+                       np.where(kind == 1, rng.integers(1, 257, size=B), rng.integers(257, 4001, size=B)))
+    max_len = int(lengths.max()) + int(rng.choice([0, 0, 1, 300]))
+    mag = float(rng.choice([1.0, 3.0]))
+    slots = 12000
+    print(f"decode random {seed}: B={B} hq={hq} hkv={hkv} d={head_dim} max_len={max_len} mag={mag}", flush=True)
+    k = (torch.randn((slots, hkv, head_dim), generator=g) * mag).to(torch.bfloat16).to(device)
+    v = torch.randn((slots, hkv, head_dim), generator=g).to(torch.bfloat16).to(device)
+    indptr = np.concatenate(([0], np.cumsum(lengths))).astype(np.int32)
+    idx = rng.integers(0, slots, size=indptr[-1]).astype(np.int32)
+    q = (torch.randn((B, hq, head_dim), generator=g) * mag).to(torch.bfloat16).to(device)
+    sinks = (torch.randn(hq, generator=g) * 2).to(device) if rng.random() < 0.5 else None
+    out_dtype = torch.float32 if rng.random() < 0.5 else torch.bfloat16
+    out = torch.full((B, hq, head_dim), 7.0, dtype=out_dtype, device=device)
+    scale = head_dim ** -0.5
+    attention.decode_attention(q, k, v, torch.from_numpy(indptr).to(device), torch.from_numpy(idx).to(device),
+                               out, scale=scale, max_len=max_len, sinks=sinks)
+    torch.cuda.synchronize()
+    got, kk, vv, qq = _f32(out), _f32(k), _f32(v), _f32(q)
+    s_np = _f32(sinks) if sinks is not None else None
+    for b, n in enumerate(lengths):
+        sel = idx[indptr[b] : indptr[b + 1]]
+        want = oat.decode_attention(qq[b], kk[sel], vv[sel], scale, s_np)
+        err = np.abs(got[b] - want).max()
+        assert err <= TOL, f"request {b} (len {n}) max err {err}"
+
+
 def test_gpt_oss_decode_after_drop_and_reposition(device):
     """32 requests x 32k tokens: compaction -> Reposition -> full / 128-window
     metadata -> one decode step on a sliding-window and a full layer."""
