@@ -142,6 +142,28 @@ def test_odd_rotary_goes_generic(device):
     _run_case(device, head_dim=40, rotary_dim=10, seed=10, table_kind="plain")
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_random_cases(device, seed):
+    # seeded random geometry and options: layers, heads, head_dim, partial
+    # rotary widths, KV and table dtypes, pair style, table kind, unmapped
+    # and same-position pairs, misaligned bases and padded slot strides
+    rng = np.random.default_rng(900 + seed)
+    head_dim = int(rng.choice([16, 32, 40, 64, 128]))
+    rotary_dim = int(rng.choice([head_dim, head_dim, 2 * int(rng.integers(1, head_dim // 2 + 1))]))
+    moved = int(rng.integers(1, 300))
+    case = dict(layers=int(rng.integers(1, 41)), heads=int(rng.choice([1, 2, 3, 4, 8])), head_dim=head_dim,
+                rotary_dim=rotary_dim, kv_dtype=[torch.bfloat16, torch.float16, torch.float32][rng.integers(0, 3)],
+                table_dtype=[torch.float32, torch.bfloat16, torch.float16][rng.integers(0, 3)],
+                neox=bool(rng.integers(0, 2)), slots=2 * moved + int(rng.integers(2, 200)), moved=moved,
+                seed=900 + seed, skip_unmapped=bool(rng.random() < 0.3), same_every=int(rng.choice([0, 0, 2, 5])),
+                misalign=bool(rng.random() < 0.2), slot_stride_extra=int(rng.choice([0, 0, 0, 8, 3])),
+                table_kind=str(rng.choice(["yarn", "plain"])))
+    if case["misalign"]:
+        case["slot_stride_extra"] = 0
+    print(f"reposition random {seed}: " + ", ".join(f"{k}={v}" for k, v in case.items()), flush=True)
+    _run_case(device, **case)
+
+
 def test_tiny_workload_bit_exact(device):
     case = single_request("tiny", device)
     w = case["workload"]
