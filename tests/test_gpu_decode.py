@@ -94,6 +94,40 @@ def test_window_and_dense_table_match_oracle(device, window):
         np.testing.assert_array_equal(d[b, : want_len[b]], full[s:])
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_registry_batches(device, seed):
+    # seeded random batches of ordinary and compacted rows: full read
+    # indices (int32 / int64) and a random window, list and dense forms
+    rng = np.random.default_rng(800 + seed)
+    batch = int(rng.integers(1, 41))
+    window = int(rng.choice([0, 1, int(rng.integers(2, 3000))]))
+    print(f"registry random {seed}: batch={batch} window={window}", flush=True)
+    table, reg, row_ids, lengths, expect = _batch(device, seed=800 + seed, batch=batch)
+    seq = torch.from_numpy(lengths).to(device)
+    indptr = torch.empty(batch + 1, dtype=torch.int32, device=device)
+    pt.build_indptr(seq, indptr)
+    out = torch.full((int(lengths.sum()),), -9, dtype=[torch.int32, torch.int64][seed % 2], device=device)
+    pt.context_decode_indices(reg.rows, table, row_ids, seq, indptr, out)
+    want_len = dec.window_lengths(reg.rows.cpu().numpy(), row_ids.cpu().numpy(), lengths, window, memory=reg.host)
+    wbuf = torch.zeros(batch + 8, dtype=torch.int32, device=device)
+    wout = torch.zeros(int(want_len.sum()) + 5, dtype=torch.int64, device=device)
+    wptr, got_len, _ = window_indices(reg.rows, table, row_ids, seq, window, wbuf, wout)
+    dense = torch.full((batch, 3000), -1, dtype=torch.int32, device=device)
+    dlen = dense_indices(reg.rows, table, row_ids, seq, dense, window=window)
+    torch.cuda.synchronize()
+    ip, got = indptr.cpu().numpy(), out.cpu().numpy()
+    np.testing.assert_array_equal(ip, dec.kv_indptr(lengths))
+    np.testing.assert_array_equal(got_len.cpu().numpy(), want_len)
+    np.testing.assert_array_equal(dlen.cpu().numpy(), want_len)
+    wip, wgot, d = wptr.cpu().numpy(), wout.cpu().numpy(), dense.cpu().numpy()
+    np.testing.assert_array_equal(wip, dec.kv_indptr(want_len))
+    for b, (_, full, _) in enumerate(expect):
+        np.testing.assert_array_equal(got[ip[b] : ip[b + 1]], full, err_msg=f"request {b}")
+        s = int(lengths[b]) - int(want_len[b])
+        np.testing.assert_array_equal(wgot[wip[b] : wip[b + 1]], full[s:], err_msg=f"window of request {b}")
+        np.testing.assert_array_equal(d[b, : want_len[b]], full[s:], err_msg=f"dense row {b}")
+
+
 def test_mapping_translation_and_row_slots(device):
     table, reg, row_ids, lengths, expect = _batch(device, seed=2, batch=6)
     mapping = (torch.arange(10**7, dtype=torch.int64) * 5 + 3).to(device)
