@@ -79,6 +79,18 @@ def test_batched_multi_stage_programs(device):
     _check(reqs, *_bind_batch(device, reqs, rng))
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_batches(device, seed):
+    # seeded random batches of random multi-stage programs: 1-60 requests of
+    # 8-3000 tokens (programs need a few tokens), a few long ones among many short
+    rng = np.random.default_rng(1100 + seed)
+    B = int(rng.integers(1, 61))
+    lengths = np.where(rng.random(B) < 0.8, rng.integers(8, 300, size=B), rng.integers(300, 3001, size=B))
+    print(f"bind random {seed}: B={B} tokens={int(lengths.sum())}", flush=True)
+    reqs = [_request(rng, int(n)) for n in lengths]
+    _check(reqs, *_bind_batch(device, reqs, rng))
+
+
 def test_long_request_spans_many_tiles(device):
     rng = np.random.default_rng(12)
     reqs = [_request(rng, 20000), _request(rng, 12), _request(rng, 3000)]
