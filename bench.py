@@ -935,8 +935,12 @@ def host_info(threads):
     sockets = int(info.get("Socket(s)", "0") or 0)
     # a virtual machine may report only the vendor line as the model name:
     # the family / model / stepping numbers identify the part
+    family = info.get("CPU family", "?")
     return {"cpu": info.get("Model name", ""),
             "cpu_family_model_stepping": "/".join(info.get(k, "?") for k in ("CPU family", "Model", "Stepping")),
+            # AMD family 26 (1Ah) is the Zen 5 core of the EPYC 9005 series
+            "cpu_core_generation": "Zen 5 (EPYC 9005 series)" if family == "26" and "AMD" in info.get(
+                "Vendor ID", "") + info.get("Model name", "") else None,
             "physical_cores": cores_per_socket * sockets or None,
             "logical_cpus": os.cpu_count(), "cpus_available": len(os.sched_getaffinity(0)),
             "torch_threads": threads}
