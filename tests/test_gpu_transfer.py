@@ -98,3 +98,30 @@ def test_row_sizes_and_layer_counts(device, layers, heads, dim):
         assert torch.equal(_bits(ks2[l][dst.long()]), _bits(ks[l][src.long()])), f"layer {l} K"
         assert torch.equal(_bits(vs2[l][dst.long()]), _bits(vs[l][src.long()])), f"layer {l} V"
         assert torch.equal(_bits(vs2[l][untouched]), _bits(before[l][untouched])), f"layer {l} V untouched"
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_copies(device, seed):
+    # seeded random geometry: layers, heads, head dims (rows of 1 to 512
+    # 16-byte chunks), padded source strides, copy counts
+    rng = np.random.default_rng(1200 + seed)
+    layers = int(rng.integers(1, 41))
+    heads = int(rng.choice([1, 2, 3, 4, 8]))
+    dim = int(rng.choice([8, 16, 24, 40, 64, 128, 256]))
+    pad = int(rng.choice([0, 0, 8, 64]))
+    slots = int(rng.integers(200, 4000))
+    n = int(rng.integers(1, slots // 2))
+    print(f"transfer random {seed}: layers={layers} heads={heads} dim={dim} pad={pad} slots={slots} n={n}", flush=True)
+    ks, vs, kp, vp = _pool(device, layers, slots, heads, dim, seed=1200 + seed, pad=pad)
+    ks2, vs2, kp2, vp2 = _pool(device, layers, slots, heads, dim, seed=1300 + seed)
+    src = torch.from_numpy(rng.choice(slots, size=n, replace=False).astype(np.int32)).to(device)
+    dst = torch.from_numpy(rng.choice(slots, size=n, replace=False).astype(np.int32)).to(device)
+    before_k = [t.clone() for t in ks2]
+    transfer.copy_kv_rows(kp, vp, ks[0], kp2, vp2, ks2[0], n, src_slots=src, dst_slots=dst)
+    torch.cuda.synchronize()
+    untouched = torch.ones(slots, dtype=torch.bool, device=device)
+    untouched[dst.long()] = False
+    for l in range(layers):
+        assert torch.equal(_bits(ks2[l][dst.long()]), _bits(ks[l][src.long()])), f"layer {l} K"
+        assert torch.equal(_bits(vs2[l][dst.long()]), _bits(vs[l][src.long()])), f"layer {l} V"
+        assert torch.equal(_bits(ks2[l][untouched]), _bits(before_k[l][untouched])), f"layer {l} K untouched"
