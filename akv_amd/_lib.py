@@ -18,6 +18,9 @@ AKV_EHIP = -5
 AKV_ERUNTIME = -71
 AKV_F32, AKV_F16, AKV_BF16 = 0, 1, 2
 AKV_I32, AKV_I64 = 0, 1
+# status word of akv_compact_rows
+AKV_STATUS_SIZES, AKV_STATUS_INCOMPLETE, AKV_STATUS_REBUILT = 1, 2, 4
+AKV_STATUS_UNUSABLE = AKV_STATUS_SIZES | AKV_STATUS_INCOMPLETE
 
 _P = c_void_p
 _SIGNATURES = {
@@ -27,6 +30,11 @@ _SIGNATURES = {
         c_int32,
         [_P, _P, c_int32, c_int32, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64,
          c_int64, _P, _P, _P, c_int64, c_int64, _P, c_int32, c_int64, c_int32, c_int32, _P],
+    ),
+    "akv_reposition_kv_layers_gated": (
+        c_int32,
+        [_P, _P, c_int32, c_int32, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64,
+         c_int64, _P, _P, _P, c_int64, c_int64, _P, c_int32, c_int64, c_int32, c_int32, _P, _P],
     ),
     "akv_compact_workspace_bytes": (c_int64, [c_int32, c_int64]),
     "akv_compact_launches": (c_int32, [c_int32, c_int64, c_int64, _P]),
@@ -43,7 +51,7 @@ _SIGNATURES = {
     "akv_decode_indices": (
         c_int32,
         [_P, _P, c_int64, _P, c_int32, _P, c_int32, _P, c_int32, _P, c_int32, _P, c_int32,
-         _P, c_int32, c_int64, c_int32, _P],
+         _P, c_int32, c_int64, c_int32, _P, _P],
     ),
     "akv_window_lengths": (
         c_int32,
@@ -66,13 +74,13 @@ _SIGNATURES = {
         c_int32,
         [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int32, c_int32,
          c_int32, c_int32, _P, _P, _P, ctypes.c_float, _P, c_int32, c_int64, c_int64, c_int64,
-         _P, c_int64, _P],
+         _P, c_int64, _P, _P],
     ),
     "akv_decode_attention_noalloc_max_bytes": (c_int64, []),
     "akv_decode_attention_noalloc": (
         c_int32,
         [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int32, c_int32,
-         c_int32, c_int32, _P, _P, _P, ctypes.c_float, _P, c_int32, c_int64, c_int64, c_int64, _P],
+         c_int32, c_int32, _P, _P, _P, ctypes.c_float, _P, c_int32, c_int64, c_int64, c_int64, _P, _P],
     ),
     "akv_context_attention": (
         c_int32,
@@ -88,7 +96,7 @@ _SIGNATURES = {
     ),
     "akv_copy_kv_rows": (
         c_int32,
-        [_P, _P, _P, _P, c_int32, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, c_int64, _P],
+        [_P, _P, _P, _P, c_int32, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, c_int64, _P, _P],
     ),
     "akv_plan_ownership": (
         c_int32,

@@ -94,10 +94,11 @@ struct CompactArgs {
   int32_t* counts;
   int32_t* status;
   int4* tile_agg;      // [tiles] per-tile aggregates (kept, moved, retired, generated)
-  uint32_t* tile_pack; // [tiles] one-launch path: kept | moved << 16 of each tile
+  uint64_t* tile_pack; // [tiles] one-launch path: tagged kept, moved of each tile
   int2* tile_pre;      // [tiles + 1] one-launch path: kept, moved before each tile
-  int2* req_local;     // [B] one-launch path: kept, moved of a request's first tile before it
-  uint32_t* sync;      // one-launch path: barrier words, zero at rest
+  uint64_t* req_local; // [B] one-launch path: tagged kept, moved of a request's first tile before it
+  uint32_t* tile_fail; // [kFusedMaxTiles] one-launch path: tag of the call in which the tile withdrew
+  uint32_t* sync;      // one-launch path: barrier words, zero before first use
   int32_t groups;      // one-launch path: arrival groups
   int64_t* req_gen;    // [B + 1] generated prefix: of every request (staged batches, count
                        // launch), of the tile's requests (others, tiles with more
@@ -526,9 +527,9 @@ __device__ __forceinline__ void fill_window(const Requests<STEPS, STAGED>& rq, c
 }
 
 // Every output of the tile, from its exclusive prefix `sums` and, when
-// spans_in, the start counts of request w0.  With write_status the last
-// tile also writes the status word.  A token's kept flag comes from the
-// tile's ballots, and its rank among retired tokens from the identity
+// spans_in, the start counts of request w0.  With status_bits >= 0 the last
+// tile also writes the status word: its size check (bit 0) | status_bits.
+// A token's kept flag comes from the tile's ballots, and its rank among retired tokens from the identity
 // retired-before = tokens-before - kept-before + moved-before.  SMALL
 // batches (positions and output sizes below 2^29) keep token positions and
 // ranks in 32 bits.
@@ -537,7 +538,7 @@ __device__ __forceinline__ void tile_outputs(const CompactArgs& a, Tile<STEPS, S
                                              const TileRequests& r, int64_t tile, int64_t t0, int64_t t1,
                                              const int64_t (&sums)[kCounters], const int64_t (&span_start)[3],
                                              const int32_t (&bps)[STEPS], const int32_t (&fps)[STEPS],
-                                             const int32_t (&slot0)[STEPS], bool write_status) {
+                                             const int32_t (&slot0)[STEPS], int status_bits) {
   using T = Tile<STEPS, STAGED>;
   const int w = threadIdx.x >> 6;
   const TileMasks<T::kBlks>& m = sh.m;
@@ -589,13 +590,13 @@ __device__ __forceinline__ void tile_outputs(const CompactArgs& a, Tile<STEPS, S
     if (r.count >= 0 && r.own_lo > 0 && threadIdx.x == 0) win.gen[0] = sums[3] - rq.gen(r.w0);
     gen_total = carry;  // the last tile's carry: every generated entry
   }
-  if (write_status && tile == a.tiles - 1 && threadIdx.x == 0 && a.status) {
+  if (status_bits >= 0 && tile == a.tiles - 1 && threadIdx.x == 0 && a.status) {
     const int64_t kept = sums[0] + m.before[T::kBlks][0];
     const int64_t moved = sums[1] + m.before[T::kBlks][1];
     const int64_t retired = sums[2] + m.before[T::kBlks][2];
     const bool bad = moved != a.fresh_count || kept > a.kept_capacity || retired > a.retired_capacity ||
                      (a.kv_indices && kept + gen_total > a.kv_capacity);
-    a.status[0] = bad ? 1 : 0;
+    a.status[0] = (bad ? 1 : 0) | status_bits;
   }
 
   // requests that end in the tile: counts and last-page lengths
@@ -854,34 +855,40 @@ __global__ void __launch_bounds__(kThreads) scatter_kernel(const CompactArgs a) 
   int64_t start_w0[3];
 #pragma unroll
   for (int c = 0; c < 3; ++c) start_w0[c] = r.spans_in ? span_start[c] : 0;
-  tile_outputs<STEPS, STAGED, false>(a, sh, win, r, tile, t0, t1, sums, start_w0, bps, fps, slot0, true);
+  tile_outputs<STEPS, STAGED, false>(a, sh, win, r, tile, t0, t1, sums, start_w0, bps, fps, slot0, 0);
 }
 
-// ---- One-launch path: every tile resident at once ------------------------
+// ---- One-launch path -------------------------------------------------------
 //
 // A tile loads its inputs once, publishes its kept and moved counts (and,
 // for the requests that start in it, their counts before their first token;
 // retired counts follow from tokens - kept + moved) and arrives at its
 // group: 64 consecutive tiles.  The last tile to arrive in group k sums the
 // group's counts, publishes the group's totals, reads the totals of groups
-// 0 .. k-1 (one lane each), writes its tiles' exclusive prefixes and
-// releases the group; each tile then writes its outputs.  Groups release in
-// order as they fill, so the first tiles write while later ones still load.
+// 0 .. k-1 (one lane each), writes its tiles' exclusive prefixes (and, for
+// the request holding the group's first token when it started in an earlier
+// group, that request's start counts) and releases the group; each tile then
+// writes its outputs.  Groups release in order as they fill, so the first
+// tiles write while later ones still load.
 //
-// Per call every tile reads the epoch word E; group records and release
-// words carry the tag E + 1, so nothing but the arrival counters needs
-// resetting between calls; the last group's releaser advances E, after every
-// tile has read it.  Arrival counters are reset by each group's last
-// arrival, so the workspace must be zero before its first use.  What crosses
-// tiles (counts, prefixes, records, release words, the status word) moves by
-// agent-scope atomic loads and stores, ordered by waiting for completion; no
-// cache-wide fence is needed.  Waits are bounded: a tile that stops waiting
-// cancels its group's release word by compare-and-swap, so a release and a
-// withdrawal exclude each other; a withdrawn tile skips its outputs and sets
-// bit 2 of the status word.  Tile 0 sets the status word to 2 first; the last
-// group clears that bit when its look-back completes.  All tiles of one
-// launch fit on the device at once (the host checks occupancy), so waits end
-// in practice long before the bound.
+// Every value one tile publishes for another carries the call's tag, epoch
+// + 1 (finish_kernel advances the epoch once per call): tile counts, request
+// start counts, group records and release words.  A reader therefore tells
+// this call's values from earlier calls' and waits (bounded) until they are
+// current; only the arrival counters are reset between calls (by each
+// group's last arrival; the workspace is zero-filled before first use).
+// Cross-tile values move by agent-scope atomic loads and stores, ordered by
+// waiting for their completion: no cache-wide fence.
+//
+// Waits are bounded.  A tile whose wait runs out cancels its group's release
+// word by compare-and-swap (a release and a withdrawal exclude each other),
+// skips its outputs, records itself in the workspace and sets bit 2 of the
+// status word.  finish_kernel, launched right after on the same stream,
+// rebuilds the outputs of every withdrawn tile from the counts that every
+// tile published, so the outputs are complete once the call's launches have
+// run, whether or not all tiles could be resident at once (kernels of other
+// streams holding CUs, a device smaller than the host assumed).  The host's
+// residency check only picks the fast path; correctness does not rest on it.
 
 constexpr int kGroupTiles = 64;  // tiles per group: one lane each
 constexpr int kMaxGroups = 32;
@@ -890,7 +897,10 @@ constexpr uint32_t kCancelled = 0x80000000u;
 constexpr uint32_t kTagMask = 0x0fffffffu;
 constexpr uint32_t kPollLimit = 1u << 20;  // ~1 s of polling at most
 constexpr int64_t kFusedMaxTiles = static_cast<int64_t>(kGroupTiles) * kMaxGroups;
-constexpr int64_t kSyncBytes = static_cast<int64_t>(3 * kMaxGroups + 1) * kSyncStride * 4;
+// arrival counters, group records, release words, the epoch and the fail
+// word (one line each), then the groups' span start counts
+constexpr int kSpanWord = (3 * kMaxGroups + 2) * kSyncStride;
+constexpr int64_t kSyncBytes = static_cast<int64_t>(kSpanWord + 2 * kMaxGroups) * 4;
 
 // Data that one tile writes and another reads within the launch goes through
 // agent-scope atomic loads and stores, which the device keeps coherent across
@@ -906,6 +916,15 @@ __device__ __forceinline__ int2 get_pair(const int2* p) {
   return make_int2(static_cast<int32_t>(static_cast<uint32_t>(v)), static_cast<int32_t>(static_cast<uint32_t>(v >> 32)));
 }
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8)); }
+__device__ __forceinline__ uint64_t load64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ uint32_t* arrive_word(const CompactArgs& a, int k) { return a.sync + k * kSyncStride; }
 __device__ __forceinline__ uint64_t* record_word(const CompactArgs& a, int k) {
@@ -915,6 +934,22 @@ __device__ __forceinline__ uint32_t* release_word(const CompactArgs& a, int k) {
   return a.sync + (2 * kMaxGroups + k) * kSyncStride;
 }
 __device__ __forceinline__ uint32_t* epoch_word(const CompactArgs& a) { return a.sync + 3 * kMaxGroups * kSyncStride; }
+__device__ __forceinline__ uint32_t* fail_word(const CompactArgs& a) {
+  return a.sync + (3 * kMaxGroups + 1) * kSyncStride;
+}
+__device__ __forceinline__ int2* span_word(const CompactArgs& a, int k) {
+  return reinterpret_cast<int2*>(a.sync + kSpanWord) + k;
+}
+
+// Tagged counts of a tile or of a request's first tile: tag in bits 32..63,
+// moved in 16..31, kept in 0..15 (a tile holds at most 2048 tokens).
+__device__ __forceinline__ uint64_t make_counts(uint32_t tag, int32_t kept, int32_t moved) {
+  return (static_cast<uint64_t>(tag) << 32) | (static_cast<uint64_t>(static_cast<uint32_t>(moved)) << 16) |
+         static_cast<uint32_t>(kept);
+}
+__device__ __forceinline__ uint32_t counts_tag(uint64_t v) { return static_cast<uint32_t>(v >> 32); }
+__device__ __forceinline__ int32_t counts_kept(uint64_t v) { return static_cast<int32_t>(v & 0xffffu); }
+__device__ __forceinline__ int32_t counts_moved(uint64_t v) { return static_cast<int32_t>((v >> 16) & 0xffffu); }
 
 // A group record: tag in bits 36..63, kept tokens in 18..35, moved in 0..17
 // (a group holds at most 64 x 2048 tokens).
@@ -922,20 +957,16 @@ __device__ __forceinline__ uint64_t make_record(uint32_t tag, uint32_t kept, uin
   return (static_cast<uint64_t>(tag) << 36) | (static_cast<uint64_t>(kept) << 18) | moved;
 }
 
-__device__ __forceinline__ void mark_withdrawn(const CompactArgs& a) {
-  if (a.status) __hip_atomic_fetch_or(reinterpret_cast<uint32_t*>(a.status), 4u, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Thread 0 of a waiting tile: polls the group's release word, read as v0
-// before arriving.  True once released with `tag`; false when this tile
-// withdrew (the wait ran out) or the group was cancelled.
-__device__ bool wait_release(uint32_t* word, uint32_t v0, uint32_t tag) {
+// Thread 0 of a waiting tile: polls the group's release word.  True once
+// released with `tag`; false when the group was cancelled or this tile
+// withdrew (its wait ran out and it cancelled the group).
+__device__ bool wait_release(uint32_t* word, uint32_t tag) {
   for (uint32_t polls = 0;; ++polls) {
-    const uint32_t v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (v != v0) return v == tag;
+    const uint32_t v = load32(word);
+    if (v == tag) return true;
+    if (v == (tag | kCancelled)) return false;
     if (polls >= kPollLimit) {
-      uint32_t expected = v0;
+      uint32_t expected = v;
       if (__hip_atomic_compare_exchange_strong(word, &expected, tag | kCancelled, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT))
         return false;
@@ -946,42 +977,82 @@ __device__ bool wait_release(uint32_t* word, uint32_t v0, uint32_t tag) {
 }
 
 // Wave 0 of the last tile to arrive in group k: the group's totals, the
-// totals of every earlier group, its tiles' prefixes, the release.  Returns
+// totals of every earlier group, its tiles' prefixes, the start counts of
+// the request that spans into the group, the release.  Returns
 // (wave-uniform) whether the tiles' prefixes were written.
 template <int STEPS>
-__device__ bool release_group(const CompactArgs& a, const Tile<STEPS, true>& sh, int k, uint32_t tag, uint32_t epoch) {
+__device__ bool release_group(const CompactArgs& a, const Tile<STEPS, true>& sh, int k, uint32_t tag) {
+  using T = Tile<STEPS, true>;
   const int lane = lane_id();
   const int64_t first = static_cast<int64_t>(k) * kGroupTiles;
   const int count = static_cast<int>(a.tiles - first < kGroupTiles ? a.tiles - first : kGroupTiles);
   const int groups = a.groups;
-  // this group's tiles, one per lane
-  const uint32_t v =
-      __hip_atomic_load(a.tile_pack + first + (lane < count ? lane : count - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int32_t kt = lane < count ? static_cast<int32_t>(v & 0xffffu) : 0;
-  const int32_t mt = lane < count ? static_cast<int32_t>(v >> 16) : 0;
-  const int32_t k_in = __ockl_wfscan_add_i32(kt, false);
-  const int32_t m_in = __ockl_wfscan_add_i32(mt, false);
-  const int32_t k_sum = __shfl(k_in + kt, 63);
-  const int32_t m_sum = __shfl(m_in + mt, 63);
-  if (lane == 0)
-    __hip_atomic_store(record_word(a, k), make_record(tag, static_cast<uint32_t>(k_sum), static_cast<uint32_t>(m_sum)),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // look back: the totals of groups 0 .. k-1, one lane each
-  int64_t bk = 0, bm = 0;
+  const int n = a.n_requests;
+  // this group's tile counts, one per lane: every tile of the group has
+  // arrived, so they are current unless the arrival counter was stale
+  int32_t kt = 0, mt = 0;
   bool ok = true;
-  if (lane < k) {
-    uint64_t rec = 0;
+  {
+    const int64_t i = first + (lane < count ? lane : 0);
     for (uint32_t polls = 0;; ++polls) {
-      rec = __hip_atomic_load(record_word(a, lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (static_cast<uint32_t>(rec >> 36) == tag) break;
+      const uint64_t v = load64(a.tile_pack + i);
+      const bool have = lane >= count || counts_tag(v) == tag;
+      kt = lane < count ? counts_kept(v) : 0;
+      mt = lane < count ? counts_moved(v) : 0;
+      if (__ballot(!have) == 0) break;
       if (polls >= kPollLimit) {
         ok = false;
         break;
       }
       __builtin_amdgcn_s_sleep(2);
     }
-    bk = static_cast<int64_t>((rec >> 18) & 0x3ffffu);
-    bm = static_cast<int64_t>(rec & 0x3ffffu);
+  }
+  const int32_t k_in = __ockl_wfscan_add_i32(kt, false);
+  const int32_t m_in = __ockl_wfscan_add_i32(mt, false);
+  const int32_t k_sum = __shfl(k_in + kt, 63);
+  const int32_t m_sum = __shfl(m_in + mt, 63);
+  if (lane == 0 && ok)
+    __hip_atomic_store(record_word(a, k), make_record(tag, static_cast<uint32_t>(k_sum), static_cast<uint32_t>(m_sum)),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // The request holding the group's first token: when it started in an
+  // earlier group g0 (tile j0), its start counts are g0's base + the counts
+  // of g0's tiles before j0 + its own counts in tile j0, all published by
+  // complete groups; read with the look-back.
+  const int64_t t_first = first * T::kTile;
+  int64_t w = wave_count_le(static_cast<int64_t>(n) + 1, t_first, [&](int64_t i) { return sh.s_off[i]; }) - 1;
+  if (w > n - 1) w = n - 1;
+  if (w < 0) w = 0;
+  const int64_t lo = sh.s_off[w];
+  const int64_t j0 = lo / T::kTile;
+  const int g0 = static_cast<int>(j0 / kGroupTiles);
+  const bool cross = lo < t_first && g0 < k;
+  const bool in_start = cross && static_cast<int64_t>(g0) * kGroupTiles + lane < j0;
+  // look back: the totals of groups 0 .. k-1 (one lane each), the start
+  // group's tile counts before j0 (one lane each), the request's own counts
+  int64_t bk = 0, bm = 0;
+  int32_t sk = 0, sm = 0, lk = 0, lm = 0;
+  if (ok) {
+    const int ir = lane < k ? lane : 0;
+    const int64_t is = cross ? static_cast<int64_t>(g0) * kGroupTiles + lane : 0;
+    for (uint32_t polls = 0;; ++polls) {
+      const uint64_t rec = load64(record_word(a, ir));
+      const uint64_t vs = load64(a.tile_pack + is);
+      const uint64_t vl = load64(a.req_local + w);
+      const bool have = (lane >= k || static_cast<uint32_t>(rec >> 36) == tag) &&
+                        (!in_start || counts_tag(vs) == tag) && (!cross || counts_tag(vl) == tag);
+      bk = lane < k ? static_cast<int64_t>((rec >> 18) & 0x3ffffu) : 0;
+      bm = lane < k ? static_cast<int64_t>(rec & 0x3ffffu) : 0;
+      sk = in_start ? counts_kept(vs) : 0;
+      sm = in_start ? counts_moved(vs) : 0;
+      lk = counts_kept(vl);
+      lm = counts_moved(vl);
+      if (__ballot(!have) == 0) break;
+      if (polls >= kPollLimit) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
   }
   const bool all_ok = __ballot(!ok) == 0;
   const int64_t base_k = __ockl_wfred_add_i64(bk);
@@ -990,67 +1061,46 @@ __device__ bool release_group(const CompactArgs& a, const Tile<STEPS, true>& sh,
     if (lane < count) put_pair(a.tile_pre + first + lane, static_cast<int32_t>(base_k + k_in), static_cast<int32_t>(base_m + m_in));
     if (k == groups - 1 && lane == 0)
       put_pair(a.tile_pre + a.tiles, static_cast<int32_t>(base_k + k_sum), static_cast<int32_t>(base_m + m_sum));
+    if (cross) {
+      const int64_t span_k = __ockl_wfred_add_i64((lane < g0 ? bk : 0) + sk) + lk;
+      const int64_t span_m = __ockl_wfred_add_i64((lane < g0 ? bm : 0) + sm) + lm;
+      if (lane == 0) put_pair(span_word(a, k), static_cast<int32_t>(span_k), static_cast<int32_t>(span_m));
+    }
     wait_stores();
   }
   if (lane == 0) {
-    // release (or cancel) the group: at most one withdrawal can change the word first
+    // release (or cancel) the group; at most one withdrawal can change the
+    // word first, after which the group stays cancelled
     uint32_t* word = release_word(a, k);
-    uint32_t cur = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bool cancelled = true;  // stays so only if every attempt fails, which no withdrawal can cause
-    for (int t = 0; t < 3; ++t) {
+    const uint32_t want = all_ok ? tag : (tag | kCancelled);
+    uint32_t cur = load32(word);
+    for (int t = 0; t < 3 && cur != (tag | kCancelled); ++t) {
       uint32_t expected = cur;
-      if (__hip_atomic_compare_exchange_strong(word, &expected, all_ok ? tag : (tag | kCancelled), __ATOMIC_RELAXED,
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-        cancelled = cur == (tag | kCancelled);
+      if (__hip_atomic_compare_exchange_strong(word, &expected, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT))
         break;
-      }
       cur = expected;
     }
-    if (!all_ok || cancelled) mark_withdrawn(a);
-    if (k == groups - 1) {
-      if (all_ok && a.status) {
-        // every tile has arrived: the status word's final size check
-        const int64_t kept = base_k + k_sum, moved = base_m + m_sum;
-        const int64_t retired = a.total - kept + moved;
-        const bool bad = moved != a.fresh_count || kept > a.kept_capacity || retired > a.retired_capacity ||
-                         (a.kv_indices && kept + sh.s_genx[a.n_requests] > a.kv_capacity);
-        uint32_t* st = reinterpret_cast<uint32_t*>(a.status);
-        __hip_atomic_fetch_and(st, ~2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (bad) __hip_atomic_fetch_or(st, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __hip_atomic_store(epoch_word(a), epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (k == groups - 1 && all_ok && a.status) {
+      // every tile has arrived: the status word's final size check
+      const int64_t kept = base_k + k_sum, moved = base_m + m_sum;
+      const int64_t retired = a.total - kept + moved;
+      const bool bad = moved != a.fresh_count || kept > a.kept_capacity || retired > a.retired_capacity ||
+                       (a.kv_indices && kept + sh.s_genx[a.n_requests] > a.kv_capacity);
+      uint32_t* st = reinterpret_cast<uint32_t*>(a.status);
+      __hip_atomic_fetch_and(st, ~2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (bad) __hip_atomic_fetch_or(st, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   return all_ok;
 }
 
-// Scalar registers are capped at 88 (86 reported): measured on MI355X, a
-// 256-thread kernel holds 8 workgroups per CU up to 78 reported SGPRs, 7 up
-// to 94 and 6 from 98, while the occupancy query reports 8 up to 94; the
-// host applies the measured limit (kFusedMaxPerCu).
+// The batch's request offsets, rows and generated prefix in LDS (the
+// one-launch path stages every request: at most kStagedRequests).
 template <int STEPS>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(88))) fused_kernel(const CompactArgs a) {
-  using T = Tile<STEPS, true>;
-  __shared__ T sh;
-  __shared__ Window win;
-  __shared__ uint32_t s_sync[4];  // epoch, release word before arriving, role, go
-  const int64_t tile = blockIdx.x;
-  const int64_t t0 = tile * T::kTile;
-  const int64_t t1 = t0 + T::kTile < a.total ? t0 + T::kTile : a.total;
-  const int n = a.n_requests;
-  const int k = static_cast<int>(tile / kGroupTiles);
-  if (threadIdx.x == 0) {
-    s_sync[0] = __hip_atomic_load(epoch_word(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // status bit 1 until the last group's look-back completes
-    if (tile == 0 && a.status) __hip_atomic_store(a.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  // one round of loads: the tile's inputs and flat birth slots, the batch's
-  // request offsets, rows and generated counts
-  uint8_t kb[STEPS];
-  int32_t bps[STEPS], fps[STEPS], slot0[STEPS];
-  load_inputs<STEPS>(a, t0, t1, kb, bps, fps);
-  load_birth_slots<STEPS>(a, t0, t1, slot0);
+__device__ __forceinline__ void stage_batch(const CompactArgs& a, Tile<STEPS, true>& sh) {
   constexpr int kRounds = (kStagedRequests + kThreads) / kThreads;  // B + 1 offsets
+  const int n = a.n_requests;
   int64_t gv[kRounds];
 #pragma unroll
   for (int q = 0; q < kRounds; ++q) {
@@ -1077,78 +1127,230 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(88)))
     if (i <= n) sh.s_genx[i] = gcarry + pre;
     gcarry += sum;
   }
+}
+
+// Scalar registers are capped at 88 (86 reported): measured on MI355X, a
+// 256-thread kernel holds 8 workgroups per CU up to 78 reported SGPRs, 7 up
+// to 94 and 6 from 98, while the occupancy query reports 8 up to 94; the
+// host applies the measured limit (kFusedMaxPerCu) when it picks the path.
+template <int STEPS>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(88))) fused_kernel(const CompactArgs a) {
+  using T = Tile<STEPS, true>;
+  __shared__ T sh;
+  __shared__ Window win;
+  __shared__ uint32_t s_sync[2];  // epoch, role
+  __shared__ int32_t s_go[5];     // go, the tile's prefix (kept, moved), request w0's start (kept, moved)
+  const int64_t tile = blockIdx.x;
+  const int64_t t0 = tile * T::kTile;
+  const int64_t t1 = t0 + T::kTile < a.total ? t0 + T::kTile : a.total;
+  const int n = a.n_requests;
+  const int k = static_cast<int>(tile / kGroupTiles);
+  if (threadIdx.x == 0) {
+    s_sync[0] = load32(epoch_word(a));
+    // status bit 1 until the last group's look-back completes
+    if (tile == 0 && a.status) __hip_atomic_store(a.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // one round of loads: the tile's inputs and flat birth slots, the batch's
+  // request offsets, rows and generated counts
+  uint8_t kb[STEPS];
+  int32_t bps[STEPS], fps[STEPS], slot0[STEPS];
+  load_inputs<STEPS>(a, t0, t1, kb, bps, fps);
+  load_birth_slots<STEPS>(a, t0, t1, slot0);
+  stage_batch<STEPS>(a, sh);
   const int64_t x[kWaves] = {t0 - 1, t1 - 1, t0, t1};
   tile_masks<STEPS, true>(a, sh, t0, t1, x, kb, bps, fps);
   const TileRequests r = tile_requests<STEPS, true>(a, sh, tile);
   const Requests<STEPS, true> rq{a, sh};
   fill_window<STEPS, true>(rq, r, win);
   // publish: the tile's counts, and the counts before each owned request
+  // (s_sync[0] was written before the barriers of the scans above)
+  const uint32_t tag = (s_sync[0] + 1u) & kTagMask;
   const TileMasks<T::kBlks>& m = sh.m;
   for (int64_t b = r.own_lo + threadIdx.x; b < r.own_hi && b < n; b += kThreads) {
     const int64_t q = rq.off(b) - t0;
-    put_pair(a.req_local + b, m.count_before(q, 0), m.count_before(q, 1));
+    __hip_atomic_store(a.req_local + b, make_counts(tag, m.count_before(q, 0), m.count_before(q, 1)),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (threadIdx.x == 0)
-    __hip_atomic_store(a.tile_pack + tile,
-                       static_cast<uint32_t>(m.before[T::kBlks][0]) | (static_cast<uint32_t>(m.before[T::kBlks][1]) << 16),
+    __hip_atomic_store(a.tile_pack + tile, make_counts(tag, m.before[T::kBlks][0], m.before[T::kBlks][1]),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   wait_stores();
   __syncthreads();
-  const uint32_t epoch = s_sync[0];
-  const uint32_t tag = (epoch + 1u) & kTagMask;
   if (threadIdx.x == 0) {
-    // the release word is read (and the read complete) before arriving
-    s_sync[1] = __hip_atomic_load(release_word(a, k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    wait_stores();
     const int64_t gfirst = static_cast<int64_t>(k) * kGroupTiles;
     const uint32_t gsize = static_cast<uint32_t>(a.tiles - gfirst < kGroupTiles ? a.tiles - gfirst : kGroupTiles);
     uint32_t last = 0;
     if (__hip_atomic_fetch_add(arrive_word(a, k), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gsize - 1) {
-      __hip_atomic_store(arrive_word(a, k), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      store32(arrive_word(a, k), 0u);
       last = 1;
     }
-    s_sync[2] = last;
+    s_sync[1] = last;
   }
   __syncthreads();
-  if (s_sync[2]) {
+  if (s_sync[1]) {
     if (threadIdx.x < 64) {
-      const bool ok = release_group<STEPS>(a, sh, k, tag, epoch);
-      if (threadIdx.x == 0) s_sync[3] = ok ? 1u : 0u;
+      const bool ok = release_group<STEPS>(a, sh, k, tag);
+      if (threadIdx.x == 0) s_go[0] = ok ? 1 : 0;
     }
   } else if (threadIdx.x == 0) {
-    const bool go = wait_release(release_word(a, k), s_sync[1], tag);
-    if (!go) mark_withdrawn(a);
-    s_sync[3] = go ? 1u : 0u;
+    s_go[0] = wait_release(release_word(a, k), tag) ? 1 : 0;
+  }
+  if (threadIdx.x == 0) {
+    bool go = s_go[0] != 0;
+    if (go) {
+      // the tile's prefix and, when a request spans in, its start counts:
+      // from the group's span word when it started in an earlier group, else
+      // from its first tile's prefix and its tagged counts there
+      const int2 pre = get_pair(a.tile_pre + tile);
+      s_go[1] = pre.x;
+      s_go[2] = pre.y;
+      if (r.spans_in) {
+        const int64_t j0 = rq.off(r.w0) / T::kTile;
+        if (j0 < static_cast<int64_t>(k) * kGroupTiles) {
+          const int2 sp = get_pair(span_word(a, k));
+          s_go[3] = sp.x;
+          s_go[4] = sp.y;
+        } else {
+          const int2 pj = get_pair(a.tile_pre + j0);
+          uint64_t v = 0;
+          for (uint32_t polls = 0;; ++polls) {
+            v = load64(a.req_local + r.w0);
+            if (counts_tag(v) == tag || polls >= kPollLimit) break;
+            __builtin_amdgcn_s_sleep(2);
+          }
+          go = counts_tag(v) == tag;
+          s_go[3] = pj.x + counts_kept(v);
+          s_go[4] = pj.y + counts_moved(v);
+        }
+      }
+    }
+    if (!go) {
+      // withdraw: finish_kernel rebuilds this tile's outputs
+      store32(a.tile_fail + tile, tag);
+      store32(fail_word(a), tag);
+      if (a.status) __hip_atomic_fetch_or(reinterpret_cast<uint32_t*>(a.status), 4u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    }
+    s_go[0] = go ? 1 : 0;
   }
   __syncthreads();
-  if (!s_sync[3]) return;
-  // the tile's prefix and, when a request spans in, its start counts
-  const int2 pre = get_pair(a.tile_pre + tile);
+  if (!s_go[0]) return;
   int64_t sums[kCounters];
-  sums[0] = __builtin_amdgcn_readfirstlane(pre.x);
-  sums[1] = __builtin_amdgcn_readfirstlane(pre.y);
+  sums[0] = s_go[1];
+  sums[1] = s_go[2];
   sums[2] = t0 - sums[0] + sums[1];
   sums[3] = 0;
   int64_t start_w0[3] = {0, 0, 0};
   if (r.spans_in) {
-    const int64_t lo = rq.off(r.w0);
-    const int2 pj = get_pair(a.tile_pre + lo / T::kTile);
-    const int2 loc = get_pair(a.req_local + r.w0);
-    start_w0[0] = __builtin_amdgcn_readfirstlane(pj.x + loc.x);
-    start_w0[1] = __builtin_amdgcn_readfirstlane(pj.y + loc.y);
-    start_w0[2] = lo - start_w0[0] + start_w0[1];
+    start_w0[0] = s_go[3];
+    start_w0[1] = s_go[4];
+    start_w0[2] = rq.off(r.w0) - start_w0[0] + start_w0[1];
   }
-  tile_outputs<STEPS, true, true>(a, sh, win, r, tile, t0, t1, sums, start_w0, bps, fps, slot0, false);
+  tile_outputs<STEPS, true, true>(a, sh, win, r, tile, t0, t1, sums, start_w0, bps, fps, slot0, -1);
+}
+
+// Right after the one-launch kernel, one workgroup: advances the epoch and,
+// when tiles of the call withdrew, rebuilds their outputs -- every tile's
+// prefix from the counts all tiles published, then each withdrawn tile's
+// work as in the one-launch kernel, in order.  This is the fallback, not the
+// fast path; it also resets the arrival counters and writes the final
+// status (bit 2 kept: the outputs were rebuilt).
+template <int STEPS>
+__global__ void __launch_bounds__(kThreads) finish_kernel(const CompactArgs a) {
+  using T = Tile<STEPS, true>;
+  __shared__ T sh;
+  __shared__ Window win;
+  __shared__ uint32_t s_word[2];
+  if (threadIdx.x == 0) {
+    s_word[0] = load32(epoch_word(a));
+    s_word[1] = load32(fail_word(a));
+  }
+  __syncthreads();
+  const uint32_t epoch = s_word[0];
+  const uint32_t tag = (epoch + 1u) & kTagMask;
+  if (s_word[1] != tag) {
+    if (threadIdx.x == 0) store32(epoch_word(a), epoch + 1u);
+    return;
+  }
+  // every tile's exclusive prefix
+  int64_t ck = 0, cm = 0;
+  for (int64_t base = 0; base < a.tiles; base += kThreads) {
+    const int64_t i = base + threadIdx.x;
+    const uint64_t v = load64(a.tile_pack + (i < a.tiles ? i : 0));
+    const int64_t kt = i < a.tiles ? counts_kept(v) : 0;
+    const int64_t mt = i < a.tiles ? counts_moved(v) : 0;
+    int64_t pk, sk, pm, sm;
+    block_scan(kt, sh.lds, pk, sk);
+    block_scan(mt, sh.lds, pm, sm);
+    if (i < a.tiles) put_pair(a.tile_pre + i, static_cast<int32_t>(ck + pk), static_cast<int32_t>(cm + pm));
+    ck += sk;
+    cm += sm;
+  }
+  if (threadIdx.x == 0) put_pair(a.tile_pre + a.tiles, static_cast<int32_t>(ck), static_cast<int32_t>(cm));
+  wait_stores();
+  stage_batch<STEPS>(a, sh);
+  __syncthreads();
+  const Requests<STEPS, true> rq{a, sh};
+  __shared__ uint8_t s_flag[kThreads];
+  for (int64_t base = 0; base < a.tiles; base += kThreads) {
+    // the tiles of this chunk that withdrew in this call
+    const int64_t i = base + threadIdx.x;
+    s_flag[threadIdx.x] = i < a.tiles && load32(a.tile_fail + i) == tag;
+    __syncthreads();
+    for (int u = 0; u < kThreads && base + u < a.tiles; ++u) {
+      if (!s_flag[u]) continue;
+      const int64_t tile = base + u;
+      const int64_t t0 = tile * T::kTile;
+      const int64_t t1 = t0 + T::kTile < a.total ? t0 + T::kTile : a.total;
+      uint8_t kb[STEPS];
+      int32_t bps[STEPS], fps[STEPS], slot0[STEPS];
+      load_inputs<STEPS>(a, t0, t1, kb, bps, fps);
+      load_birth_slots<STEPS>(a, t0, t1, slot0);
+      const int64_t x[kWaves] = {t0 - 1, t1 - 1, t0, t1};
+      tile_masks<STEPS, true>(a, sh, t0, t1, x, kb, bps, fps);
+      const TileRequests r = tile_requests<STEPS, true>(a, sh, tile);
+      fill_window<STEPS, true>(rq, r, win);
+      const int2 pre = get_pair(a.tile_pre + tile);
+      int64_t sums[kCounters];
+      sums[0] = __builtin_amdgcn_readfirstlane(pre.x);
+      sums[1] = __builtin_amdgcn_readfirstlane(pre.y);
+      sums[2] = t0 - sums[0] + sums[1];
+      sums[3] = 0;
+      int64_t start_w0[3] = {0, 0, 0};
+      if (r.spans_in) {
+        const int64_t lo = rq.off(r.w0);
+        const int2 pj = get_pair(a.tile_pre + lo / T::kTile);
+        const uint64_t v = load64(a.req_local + r.w0);
+        start_w0[0] = __builtin_amdgcn_readfirstlane(pj.x + counts_kept(v));
+        start_w0[1] = __builtin_amdgcn_readfirstlane(pj.y + counts_moved(v));
+        start_w0[2] = lo - start_w0[0] + start_w0[1];
+      }
+      tile_outputs<STEPS, true, true>(a, sh, win, r, tile, t0, t1, sums, start_w0, bps, fps, slot0, -1);
+    }
+    __syncthreads();
+    if (i < a.tiles && s_flag[threadIdx.x]) store32(a.tile_fail + i, 0u);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (a.status) {
+      const int64_t retired = a.total - ck + cm;
+      const bool bad = cm != a.fresh_count || ck > a.kept_capacity || retired > a.retired_capacity ||
+                       (a.kv_indices && ck + sh.s_genx[a.n_requests] > a.kv_capacity);
+      store32(reinterpret_cast<uint32_t*>(a.status), (bad ? 1u : 0u) | 4u);
+    }
+    for (int g = 0; g < kMaxGroups; ++g) store32(arrive_word(a, g), 0u);
+    store32(epoch_word(a), epoch + 1u);
+  }
 }
 
 // Byte offsets of the workspace arrays (each 128-byte aligned).
 struct Layout {
-  int64_t sync, tile_agg, tile_prefix, req_local, req_gen, req_row, bytes;
+  int64_t sync, tile_fail, tile_agg, tile_prefix, req_local, req_gen, req_row, bytes;
 };
 
-// Sized for both paths: the barrier words first (at a fixed offset, so
-// batches of any size may share a workspace), then per-tile and
-// per-request arrays.
+// Sized for both paths: the barrier words and the withdrawn-tile words
+// first (at fixed offsets, so batches of any size may share a workspace),
+// then per-tile and per-request arrays.
 Layout workspace_layout(int64_t n_requests, int64_t total) {
   const int64_t two_launch = tile_count(total, tile_steps(total));
   const int64_t per_step = (total + kThreads - 1) / kThreads;  // most tiles of the one-launch path
@@ -1162,6 +1364,7 @@ Layout workspace_layout(int64_t n_requests, int64_t total) {
     return here;
   };
   l.sync = take(kSyncBytes);
+  l.tile_fail = take(4 * kFusedMaxTiles);
   l.tile_agg = take(16 * tiles);
   l.tile_prefix = take(8 * (tiles + 1));
   l.req_local = take(8 * n_requests);
@@ -1221,16 +1424,22 @@ int fused_variant(int32_t n_requests, int64_t total_tokens, int64_t largest_list
   return -1;
 }
 
+// The one-launch kernel, then the one-workgroup finish (epoch, fallback).
+template <int STEPS>
+void launch_fused(const CompactArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((fused_kernel<STEPS>), dim3(static_cast<unsigned>(a.tiles)), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL((finish_kernel<STEPS>), dim3(1), dim3(kThreads), 0, st, a);
+}
+
 void launch_fused(int steps, const CompactArgs& a, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(a.tiles));
   switch (steps) {
-    case 1: hipLaunchKernelGGL((fused_kernel<1>), grid, dim3(kThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((fused_kernel<2>), grid, dim3(kThreads), 0, st, a); break;
-    case 3: hipLaunchKernelGGL((fused_kernel<3>), grid, dim3(kThreads), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((fused_kernel<4>), grid, dim3(kThreads), 0, st, a); break;
-    case 5: hipLaunchKernelGGL((fused_kernel<5>), grid, dim3(kThreads), 0, st, a); break;
-    case 6: hipLaunchKernelGGL((fused_kernel<6>), grid, dim3(kThreads), 0, st, a); break;
-    default: hipLaunchKernelGGL((fused_kernel<8>), grid, dim3(kThreads), 0, st, a); break;
+    case 1: launch_fused<1>(a, st); break;
+    case 2: launch_fused<2>(a, st); break;
+    case 3: launch_fused<3>(a, st); break;
+    case 4: launch_fused<4>(a, st); break;
+    case 5: launch_fused<5>(a, st); break;
+    case 6: launch_fused<6>(a, st); break;
+    default: launch_fused<8>(a, st); break;
   }
 }
 
@@ -1339,9 +1548,10 @@ extern "C" int akv_compact_rows(int32_t n_requests, const int64_t* req_offsets, 
   char* ws = static_cast<char*>(workspace);
   a.sync = reinterpret_cast<uint32_t*>(ws + lay.sync);
   a.tile_agg = reinterpret_cast<int4*>(ws + lay.tile_agg);
-  a.tile_pack = reinterpret_cast<uint32_t*>(ws + lay.tile_agg);  // the paths never share a call
+  a.tile_pack = reinterpret_cast<uint64_t*>(ws + lay.tile_agg);  // the paths never share a call
+  a.tile_fail = reinterpret_cast<uint32_t*>(ws + lay.tile_fail);
   a.tile_pre = reinterpret_cast<int2*>(ws + lay.tile_prefix);
-  a.req_local = reinterpret_cast<int2*>(ws + lay.req_local);
+  a.req_local = reinterpret_cast<uint64_t*>(ws + lay.req_local);
   a.req_gen = reinterpret_cast<int64_t*>(ws + lay.req_gen);
   a.req_row = reinterpret_cast<int32_t**>(ws + lay.req_row);
   a.total = total_tokens;

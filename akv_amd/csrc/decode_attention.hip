@@ -48,6 +48,7 @@ struct AttnArgs {
   const int32_t* kv_indptr;
   const int32_t* kv_indices;
   const float* sinks;
+  const int32_t* gate;  // compaction status word, or nullptr
   float scale_log2;  // scale * log2(e)
   void* out;
   int32_t out_f32;
@@ -75,6 +76,8 @@ __global__ void __launch_bounds__(64) decode_attention_partial_kernel(const Attn
   const int b = blockIdx.z;
   const int64_t begin = a.kv_indptr[b];
   const int64_t len = a.kv_indptr[b + 1] - begin;
+  // a closed gate stops the workgroup before its key indices and rows
+  if (gated(a.gate)) return;
   const int64_t c0 = static_cast<int64_t>(chunk) * kChunk;
   float* part = a.partial + ((static_cast<int64_t>(b) * a.kv_heads + g) * a.chunks + chunk) * 16 * (D + 2);
   const int col = lane & 15;   // head within the group (B / D layout column)
@@ -285,6 +288,7 @@ __global__ void __launch_bounds__(kCombineThreads) decode_attention_combine_kern
   const int dl = threadIdx.x % kLanes;
   const int way = threadIdx.x / kLanes;
   const int64_t len = a.kv_indptr[b + 1] - a.kv_indptr[b];
+  if (gated(a.gate)) return;
   // keys past max_len (a caller error) are not read: the partials stop there
   const int64_t want = (len + kChunk - 1) / kChunk;
   const int used = static_cast<int>(want < a.chunks ? want : a.chunks);
@@ -389,7 +393,7 @@ extern "C" int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q
                                     const int32_t* kv_indptr, const int32_t* kv_indices, const float* sinks,
                                     float scale, void* out, int32_t out_dtype, int64_t out_stride_b,
                                     int64_t out_stride_h, int64_t max_len, void* workspace,
-                                    int64_t workspace_bytes, void* stream) {
+                                    int64_t workspace_bytes, const int32_t* status, void* stream) {
   using namespace akv;
   if (n_requests < 0 || max_len < 0) return fail(AKV_EINVAL, "akv_decode_attention: negative size");
   if (n_requests == 0) return AKV_OK;
@@ -424,6 +428,7 @@ extern "C" int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q
   a.kv_indptr = kv_indptr;
   a.kv_indices = kv_indices;
   a.sinks = sinks;
+  a.gate = status;
   a.scale_log2 = scale * kLog2e;
   a.out = out;
   a.out_f32 = out_dtype == AKV_F32;
@@ -464,7 +469,7 @@ extern "C" int akv_decode_attention_noalloc(const void* q, int64_t q_stride_b, i
                                             int32_t head_dim, const int32_t* kv_indptr, const int32_t* kv_indices,
                                             const float* sinks, float scale, void* out, int32_t out_dtype,
                                             int64_t out_stride_b, int64_t out_stride_h, int64_t max_len,
-                                            void* stream) {
+                                            const int32_t* status, void* stream) {
   using namespace akv;
   const int64_t need = akv_decode_attention_workspace_bytes(n_requests, kv_heads > 0 ? kv_heads : 1,
                                                             head_dim > 0 ? head_dim : 1, max_len);
@@ -478,12 +483,12 @@ extern "C" int akv_decode_attention_noalloc(const void* q, int64_t q_stride_b, i
                                                    k_stride_head, v_stride_slot, v_stride_head, n_requests,
                                                    q_heads, kv_heads, head_dim, kv_indptr, kv_indices, sinks,
                                                    scale, out, out_dtype, out_stride_b, out_stride_h, max_len,
-                                                   nullptr, 0, stream);
+                                                   nullptr, 0, status, stream);
   void* ws = nullptr;
   const int rc = scratch_address(&ws);
   if (rc) return rc;
   return akv_decode_attention(q, q_stride_b, q_stride_h, k_buffer, v_buffer, k_stride_slot, k_stride_head,
                               v_stride_slot, v_stride_head, n_requests, q_heads, kv_heads, head_dim, kv_indptr,
                               kv_indices, sinks, scale, out, out_dtype, out_stride_b, out_stride_h, max_len, ws,
-                              kScratchBytes, stream);
+                              kScratchBytes, status, stream);
 }

@@ -35,6 +35,7 @@ struct DecodeArgs {
   void* output;
   const void* starts;
   const void* mapping;
+  const int32_t* gate;  // compaction status word, or nullptr
   int64_t multiplier;
   int32_t n_requests;
   bool rows64, lengths64, indptr64, output64, starts64, mapping64;
@@ -55,6 +56,8 @@ __global__ void __launch_bounds__(256) decode_indices_kernel(const DecodeArgs a)
   const int64_t row_pointer = entry[5];
   const int32_t* raw_row = row_pointer != 0 ? reinterpret_cast<const int32_t*>(row_pointer)
                                             : a.table + row * a.row_stride;
+  // a closed gate stops the request before its raw ids and row entries
+  if (gated(a.gate)) return;
   const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
   auto raw_of = [&](int64_t i) -> int64_t {
     const int64_t logical = start + i;
@@ -237,7 +240,8 @@ extern "C" int akv_decode_indices(const int64_t* registry, const int32_t* table,
                                   int32_t lengths_dtype, const void* indptr, int32_t indptr_dtype,
                                   void* output, int32_t output_dtype, const void* starts,
                                   int32_t starts_dtype, const void* mapping, int32_t mapping_dtype,
-                                  int64_t multiplier, int32_t n_requests, void* stream) {
+                                  int64_t multiplier, int32_t n_requests, const int32_t* status,
+                                  void* stream) {
   using namespace akv;
   if (n_requests < 0) return fail(AKV_EINVAL, "akv_decode_indices: negative batch size");
   if (n_requests == 0) return AKV_OK;
@@ -258,6 +262,7 @@ extern "C" int akv_decode_indices(const int64_t* registry, const int32_t* table,
   a.output = output;
   a.starts = starts;
   a.mapping = mapping;
+  a.gate = status;
   a.multiplier = multiplier;
   a.n_requests = n_requests;
   a.rows64 = rows_dtype == AKV_I64;

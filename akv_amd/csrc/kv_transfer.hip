@@ -37,6 +37,7 @@ struct CopyArgs {
   int64_t src_k_stride, src_v_stride, dst_k_stride, dst_v_stride;  // bytes between slots
   const int32_t* src_slots;
   const int32_t* dst_slots;
+  const int32_t* gate;  // compaction status word, or nullptr
   int64_t n;
   int32_t n_layers;
   int32_t chunks;  // 16-byte chunks per row
@@ -48,6 +49,7 @@ __global__ void __launch_bounds__(kThreads) copy_kv_rows_kernel(const CopyArgs a
   const int64_t per_token = static_cast<int64_t>(a.n_layers) * 2 * a.chunks;
   const int64_t tokens = a.n - t0 < a.tokens_per_block ? a.n - t0 : a.tokens_per_block;
   const int64_t items = tokens * per_token;
+  if (gated(a.gate)) return;
   for (int64_t base = 0; base < items; base += static_cast<int64_t>(kThreads) * kBatch) {
     u32x4 v[kBatch];
     char* dst[kBatch];
@@ -96,6 +98,8 @@ __global__ void __launch_bounds__(256) copy_rows_layer_major(const CopyArgs a, i
   const bool kv = blockIdx.y & 1;
   const int64_t s = SRC ? static_cast<int64_t>(a.src_slots[t]) : t;
   const int64_t d = DST ? static_cast<int64_t>(a.dst_slots[t]) : t;
+  // the gate is read with the slot entries and closes before the rows
+  if (gated(a.gate)) return;
   const char* src = reinterpret_cast<const char*>(kv ? a.src_v[l] : a.src_k[l]) + s * (kv ? a.src_v_stride : a.src_k_stride);
   char* dst = reinterpret_cast<char*>(kv ? a.dst_v[l] : a.dst_k[l]) + d * (kv ? a.dst_v_stride : a.dst_k_stride);
   u32x4 v[U];
@@ -146,7 +150,7 @@ extern "C" int akv_copy_kv_rows(const uint64_t* src_k_ptrs, const uint64_t* src_
                                 const uint64_t* dst_v_ptrs, int32_t n_layers, int64_t row_bytes,
                                 int64_t src_k_stride, int64_t src_v_stride, int64_t dst_k_stride,
                                 int64_t dst_v_stride, const int32_t* src_slots, const int32_t* dst_slots,
-                                int64_t n_tokens, void* stream) {
+                                int64_t n_tokens, const int32_t* status, void* stream) {
   using namespace akv;
   if (n_layers < 0 || n_tokens < 0) return fail(AKV_EINVAL, "akv_copy_kv_rows: negative size");
   if (n_layers == 0 || n_tokens == 0) return AKV_OK;
@@ -168,6 +172,7 @@ extern "C" int akv_copy_kv_rows(const uint64_t* src_k_ptrs, const uint64_t* src_
   a.dst_v_stride = dst_v_stride;
   a.src_slots = src_slots;
   a.dst_slots = dst_slots;
+  a.gate = status;
   a.n = n_tokens;
   a.n_layers = n_layers;
   a.chunks = static_cast<int32_t>(row_bytes / 16);

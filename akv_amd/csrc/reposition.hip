@@ -34,6 +34,7 @@ struct RepositionArgs {
   const int32_t* dst;
   const int32_t* pairs;
   const void* cos_sin;
+  const int32_t* gate;  // compaction status word, or nullptr
   int64_t k_stride_slot, k_stride_head, v_stride_slot, v_stride_head;
   int64_t pair_stride, rope_stride;
   int32_t n_layers, n_heads, head_dim, rotary_dim;
@@ -354,6 +355,9 @@ __global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionAr
     old_pos = pair[0];
     new_pos = pair[1];
   }
+  // the gate is read with the token's list entries; a closed gate stops the
+  // token before its table rows and K/V rows are touched
+  if (gated(a.gate)) live = false;
   mv.same = old_pos == new_pos;
   if (live && !mv.same) {
     const CS* table = static_cast<const CS*>(a.cos_sin);
@@ -423,6 +427,7 @@ __global__ void __launch_bounds__(256) reposition_generic_kernel(const Repositio
   const int H = a.n_heads;
   const int R = a.rotary_dim;
   const int half = R >> 1;
+  if (gated(a.gate)) return;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
        idx += stride) {
@@ -565,15 +570,15 @@ int dtype_bytes(int32_t d) { return d == AKV_F32 ? 4 : 2; }
 }  // namespace
 }  // namespace akv
 
-extern "C" int akv_reposition_kv_layers(const uint64_t* k_ptrs, const uint64_t* v_ptrs,
-                                        int32_t n_layers, int32_t kv_dtype, int32_t n_heads,
-                                        int32_t head_dim, int32_t rotary_dim, int64_t k_stride_slot,
-                                        int64_t k_stride_head, int64_t v_stride_slot,
-                                        int64_t v_stride_head, const int32_t* src,
-                                        const int32_t* dst, const int32_t* pairs,
-                                        int64_t pair_stride, int64_t n_tokens, const void* cos_sin,
-                                        int32_t cos_sin_dtype, int64_t rope_stride, int32_t is_neox,
-                                        int32_t skip_unmapped, void* stream) {
+extern "C" int akv_reposition_kv_layers_gated(const uint64_t* k_ptrs, const uint64_t* v_ptrs,
+                                              int32_t n_layers, int32_t kv_dtype, int32_t n_heads,
+                                              int32_t head_dim, int32_t rotary_dim, int64_t k_stride_slot,
+                                              int64_t k_stride_head, int64_t v_stride_slot,
+                                              int64_t v_stride_head, const int32_t* src,
+                                              const int32_t* dst, const int32_t* pairs,
+                                              int64_t pair_stride, int64_t n_tokens, const void* cos_sin,
+                                              int32_t cos_sin_dtype, int64_t rope_stride, int32_t is_neox,
+                                              int32_t skip_unmapped, const int32_t* status, void* stream) {
   using namespace akv;
   if (kv_dtype != AKV_F32 && kv_dtype != AKV_F16 && kv_dtype != AKV_BF16)
     return fail(AKV_EINVAL, "akv_reposition_kv_layers: unsupported KV dtype %d", kv_dtype);
@@ -601,6 +606,7 @@ extern "C" int akv_reposition_kv_layers(const uint64_t* k_ptrs, const uint64_t* 
   a.dst = dst;
   a.pairs = pairs;
   a.cos_sin = cos_sin;
+  a.gate = status;
   a.k_stride_slot = k_stride_slot;
   a.k_stride_head = k_stride_head;
   a.v_stride_slot = v_stride_slot;
@@ -638,4 +644,19 @@ extern "C" int akv_reposition_kv_layers(const uint64_t* k_ptrs, const uint64_t* 
     default:
       return launch_cs<__bf16>(a, n_tokens, cos_sin_dtype, st, vec_ok);
   }
+}
+
+extern "C" int akv_reposition_kv_layers(const uint64_t* k_ptrs, const uint64_t* v_ptrs,
+                                        int32_t n_layers, int32_t kv_dtype, int32_t n_heads,
+                                        int32_t head_dim, int32_t rotary_dim, int64_t k_stride_slot,
+                                        int64_t k_stride_head, int64_t v_stride_slot,
+                                        int64_t v_stride_head, const int32_t* src,
+                                        const int32_t* dst, const int32_t* pairs,
+                                        int64_t pair_stride, int64_t n_tokens, const void* cos_sin,
+                                        int32_t cos_sin_dtype, int64_t rope_stride, int32_t is_neox,
+                                        int32_t skip_unmapped, void* stream) {
+  return akv_reposition_kv_layers_gated(k_ptrs, v_ptrs, n_layers, kv_dtype, n_heads, head_dim, rotary_dim,
+                                        k_stride_slot, k_stride_head, v_stride_slot, v_stride_head, src, dst,
+                                        pairs, pair_stride, n_tokens, cos_sin, cos_sin_dtype, rope_stride, is_neox,
+                                        skip_unmapped, nullptr, stream);
 }

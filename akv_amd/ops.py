@@ -70,6 +70,39 @@ def reposition_kv_layers(
     wrapper does no GPU-to-CPU read and no synchronisation, and allocates no
     KV page.
     """
+    _reposition(k_data_ptrs, v_data_ptrs, k_layout, v_layout, source_slots, destination_slots, position_pairs,
+                cos_sin_cache, is_neox_style, page_size, skip_unmapped, rotary_dim, None)
+
+
+def reposition_kv_layers_gated(
+    k_data_ptrs: torch.Tensor,
+    v_data_ptrs: torch.Tensor,
+    k_layout: torch.Tensor,
+    v_layout: torch.Tensor,
+    source_slots: torch.Tensor,
+    destination_slots: torch.Tensor,
+    position_pairs: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    *,
+    status: torch.Tensor,
+    is_neox_style: bool = True,
+    page_size: int = 1,
+    skip_unmapped: bool = False,
+    rotary_dim: int | None = None,
+) -> None:
+    """``reposition_kv_layers`` behind the device status word of the
+    compaction that built the lists (``tables.compact_rows``'s
+    ``outputs.status``): every workgroup reads it and, when the lists are
+    unusable, touches no K/V row and writes nothing.  So the lists go from
+    the compaction to the Reposition on one stream with no host read."""
+    if status.dtype != torch.int32 or status.numel() < 1 or status.device != k_layout.device:
+        raise ValueError("status must be an int32 device word on the KV device")
+    _reposition(k_data_ptrs, v_data_ptrs, k_layout, v_layout, source_slots, destination_slots, position_pairs,
+                cos_sin_cache, is_neox_style, page_size, skip_unmapped, rotary_dim, status)
+
+
+def _reposition(k_data_ptrs, v_data_ptrs, k_layout, v_layout, source_slots, destination_slots, position_pairs,
+                cos_sin_cache, is_neox_style, page_size, skip_unmapped, rotary_dim, status):
     if page_size != 1:
         raise ValueError("Context Reposition requires page_size=1")
     tensors = (
@@ -135,7 +168,7 @@ def reposition_kv_layers(
         raise ValueError("Reposition cos/sin cache must be float32, float16 or bfloat16")
     lib = _lib.load()
     with _on_device(k_layout.device):
-        rc = lib.akv_reposition_kv_layers(
+        rc = lib.akv_reposition_kv_layers_gated(
             k_data_ptrs.data_ptr(),
             v_data_ptrs.data_ptr(),
             len(k_data_ptrs),
@@ -157,6 +190,7 @@ def reposition_kv_layers(
             cos_sin_cache.stride(0),
             1 if is_neox_style else 0,
             1 if skip_unmapped else 0,
+            _lib.ptr(status),
             current_stream_handle(k_layout.device),
         )
     _lib.check(rc, "akv_reposition_kv_layers")

@@ -1,17 +1,21 @@
-"""Request-local KV page ownership across prefill forwards.
+"""Request-local KV page ownership across prefill forwards: the native
+plan, advance and bind of the multi-forward occurrence planner.
 
-Mirror of ``akv/system/sglang/srt/context_system/occurrence.py:269-1006``
-(``OccurrenceMaterialization``, ``plan_occurrence_materialization``,
-``OccurrenceState``, ``OccurrenceAdvance``, ``free_context_slots``,
-``ContextPrefillCompletion``): same names, arguments, results and
-``ValueError`` messages.  A prompt may be computed in several forwards
-(chunked prefill, a matched prefix borrowed from the radix cache, recovery
-gaps, per-chunk publication).  The host decisions run in C++
-(``akv_plan_ownership`` / ``akv_advance_ownership``) on CPU metadata; slot
-values never leave the device: every list of slots a step produces is one
-segment of a single batched gather launch (``akv_gather_slots``) fed by one
-host-to-device copy, and :func:`advance_batch` binds a whole batch of
-requests with one copy and one launch.
+The reference's ``OccurrenceState`` (``akv/system/sglang/srt/context_system/
+occurrence.py:470-920``) keeps the radix-cache bookkeeping -- matched
+prefixes (``from_match``, ``reuse_match_gap``), which terminal versions a
+forward publishes (``prefill_terminal_keep``), publication and Drop of
+borrowed owners, SWA residency helpers and the release of private pages
+(``free_context_slots``, ``ContextPrefillCompletion``).  It stays the caller
+here.  What this module replaces is the hot part of a forward
+(``occurrence.py:341-466`` plan, ``:632-767`` advance and terminal slots,
+``:269-338`` bind): the host decisions run in C++ (``akv_plan_ownership`` /
+``akv_advance_ownership``) on CPU metadata, and slot values never leave the
+device: every list of slots a step produces is one segment of a single
+batched gather launch (``akv_gather_slots``) fed by one host-to-device
+copy, and :func:`advance_batch` binds a whole batch of requests with one
+copy and one launch.  Names, fields and ``ValueError`` messages of the
+calls kept here are the reference's.
 """
 
 from __future__ import annotations
@@ -263,9 +267,12 @@ class OccurrenceAdvance:
 
 @dataclass(frozen=True)
 class OccurrenceState:
-    """Request-local page ownership between prefill forwards
-    (``occurrence.py:470-920``).  CPU rows index ``slots`` (device); a row is
-    a page the request owns (``owned``) or borrows from the cache."""
+    """Request-local page ownership between prefill forwards: the fields of
+    the reference's ``OccurrenceState`` (``occurrence.py:470-490``).  CPU
+    rows index ``slots`` (device); a row is a page the request owns
+    (``owned``) or borrows from the cache.  The reference's state methods
+    that build and edit these fields outside a forward (matches, publication,
+    Drop of borrowed owners) stay the reference's."""
 
     slots: torch.Tensor
     owned: torch.Tensor
@@ -276,86 +283,20 @@ class OccurrenceState:
     swa_resident: torch.Tensor | None = None
 
     @classmethod
-    def from_match(cls, slots, positions, *, exact_prefix_len, resident=None, swa_resident=None):
-        if (
-            slots.ndim != 1
-            or slots.dtype not in (torch.int32, torch.int64)
-            or positions.device.type != "cpu"
-            or positions.dtype != torch.int32
-            or positions.shape != slots.shape
-            or not 0 <= exact_prefix_len <= len(slots)
-        ):
-            raise ValueError("Invalid Context match ownership metadata")
-        if resident is not None and (
-            resident.device.type != "cpu" or resident.dtype != torch.bool or resident.shape != slots.shape
-        ):
-            raise ValueError("Context residency must be an aligned CPU bool vector")
-        if swa_resident is not None and (
-            swa_resident.device.type != "cpu" or swa_resident.dtype != torch.bool
-            or swa_resident.shape != slots.shape
-        ):
-            raise ValueError("Context SWA residency must be an aligned CPU bool vector")
-        rows = torch.arange(len(slots), dtype=torch.int64)
-        if resident is not None:
-            rows[~resident] = -1
-        return cls(slots, torch.zeros(len(slots), dtype=torch.bool), rows,
-                   torch.full((len(slots),), -1, dtype=torch.int64), positions.clone(), exact_prefix_len,
-                   swa_resident.clone() if swa_resident is not None else None)
-
-    def reuse_match_gap(self, matched_slots, matched_positions, resident, end, *, exact_prefix_len,
-                        swa_resident=None):
-        """Borrow the resident gap ``[start, end)`` of a matched path
-        (``occurrence.py:528-586``): metadata only, no page moves."""
-        start = len(self.canonical_rows)
-        if (
-            not start <= end <= len(matched_slots)
-            or matched_positions.device.type != "cpu"
-            or matched_positions.dtype != torch.int32
-            or resident.device.type != "cpu"
-            or resident.dtype != torch.bool
-            or matched_positions.shape != matched_slots.shape
-            or resident.shape != matched_slots.shape
-            or matched_slots.ndim != 1
-            or matched_slots.dtype != self.slots.dtype
-            or matched_slots.device != self.slots.device
-            or not self.exact_prefix_len <= exact_prefix_len <= len(matched_slots)
-        ):
-            raise ValueError("Invalid matched gap ownership metadata")
-        if (self.swa_resident is None) != (swa_resident is None) or (
-            swa_resident is not None and (
-                swa_resident.device.type != "cpu" or swa_resident.dtype != torch.bool
-                or swa_resident.shape != matched_slots.shape)
-        ):
-            raise ValueError("Context matched gap must preserve SWA residency metadata")
-        if end == start:
-            return self
-        count = end - start
-        rows = torch.arange(len(self.slots), len(self.slots) + count, dtype=torch.int64)
-        rows[~resident[start:end]] = -1
-        return OccurrenceState(
-            torch.cat((self.slots, matched_slots[start:end])),
-            torch.cat((self.owned, torch.zeros(count, dtype=torch.bool))),
-            torch.cat((self.canonical_rows, rows)),
-            torch.cat((self.terminal_rows, torch.full((count,), -1, dtype=torch.int64))),
-            torch.cat((self.canonical_positions, matched_positions[start:end])),
-            min(end, exact_prefix_len),
-            torch.cat((self.swa_resident, swa_resident[start:end])) if swa_resident is not None else None,
-        )
-
-    def prefill_terminal_keep(self, layout, query_end):
-        """Raw tokens whose terminal version this forward publishes
-        (``occurrence.py:588-612``): before the final forward only versions
-        already at their final position."""
-        start = len(self.canonical_rows)
-        keep = layout.keep_mask[:query_end].clone()
-        keep[:start] &= (self.canonical_rows >= 0) | (self.terminal_rows >= 0)
-        if query_end < len(layout.positions):
-            available = layout.birth_positions[:query_end] == layout.positions[:query_end]
-            available[:start] = (self.canonical_positions == layout.positions[:start]) | (self.terminal_rows >= 0)
-            keep &= available
-        return keep
+    def empty(cls, device, slot_dtype=torch.int64, *, track_swa=False):
+        """The state of a request with no matched prefix: nothing owned,
+        nothing canonical, no terminal versions."""
+        if slot_dtype not in _SLOT_DTYPES:
+            raise ValueError("Occurrence slots must be int32 or int64")
+        none64 = torch.empty(0, dtype=torch.int64)
+        return cls(torch.empty(0, dtype=slot_dtype, device=device), torch.empty(0, dtype=torch.bool), none64,
+                   none64.clone(), torch.empty(0, dtype=torch.int32), 0,
+                   torch.empty(0, dtype=torch.bool) if track_swa else None)
 
     def plan(self, window, terminal_keep):
+        """The forward's ownership plan (``akv_plan_ownership``) over this
+        state's rows; ``terminal_keep`` is the caller's choice of the raw
+        tokens whose terminal versions the forward publishes."""
         start = len(self.canonical_rows)
         canonical = self.canonical_rows.numpy()
         present = canonical >= 0
@@ -374,115 +315,6 @@ class OccurrenceState:
     def terminal_slots(self):
         """Raw-order final-position slots, -1 for holes (``:757-767``)."""
         return _gather_one(self.slots, self.terminal_rows.numpy())
-
-    def publish(self, matched_terminal_slots, *, cache_len=None, swa_resident=None):
-        """Hand the published terminal versions to the cache's owners after
-        its insert (``occurrence.py:769-821``)."""
-        rows = self.terminal_rows.numpy()
-        if (
-            matched_terminal_slots.shape != rows.shape
-            or matched_terminal_slots.dtype != self.slots.dtype
-            or matched_terminal_slots.device != self.slots.device
-        ):
-            raise ValueError("Context publication must cover the raw terminal table")
-        if cache_len is None:
-            cache_len = len(rows)
-        if not 0 <= cache_len <= len(rows):
-            raise ValueError("Context cache publication length exceeds the raw table")
-        present = np.flatnonzero(rows[:cache_len] >= 0)
-        target = rows[present]
-        if len(np.unique(target)) != len(target):
-            raise ValueError("Distinct raw tokens cannot publish the same KV owner")
-        # slots'[i] = matched[raw of i] for published rows, else slots[i]
-        source = np.arange(len(self.slots), dtype=np.int64)
-        source[target] = len(self.slots) + present
-        g = _Gather(self.slots.device, self.slots.dtype)
-        g.add(g.request(self.slots, matched_terminal_slots), source)
-        slots = g.run()[0][0]
-        owned = self.owned.clone()
-        owned[target] = False
-        swa = self.swa_resident
-        if swa_resident is not None:
-            if swa is None or swa_resident.device.type != "cpu" or swa_resident.dtype != torch.bool \
-                    or swa_resident.shape != rows.shape:
-                raise ValueError("Context publication SWA metadata must cover the raw table")
-            swa = swa.clone()
-            swa[target] = swa_resident[present]
-        return OccurrenceState(slots, owned, self.canonical_rows, self.terminal_rows, self.canonical_positions,
-                               self.exact_prefix_len, swa)
-
-    def drop_borrowed_raw(self, dropped):
-        """Forget borrowed owners of dropped raw tokens before the cache may
-        evict them (``occurrence.py:823-864``)."""
-        if dropped.device.type != "cpu" or dropped.dtype != torch.bool or dropped.shape != self.terminal_rows.shape:
-            raise ValueError("Context Drop ownership mask must cover the raw state")
-        canonical = self.canonical_rows.numpy().copy()
-        terminal = self.terminal_rows.numpy().copy()
-        owned = self.owned.numpy()
-        mask = dropped.numpy()
-        changed = False
-        for rows in (canonical, terminal):
-            hit = np.flatnonzero(mask & (rows >= 0))
-            hit = hit[~owned[rows[hit]]]
-            if len(hit):
-                rows[hit] = -1
-                changed = True
-        if not changed:
-            return self
-        live = owned.copy()
-        live[canonical[canonical >= 0]] = True
-        live[terminal[terminal >= 0]] = True
-        retained = np.flatnonzero(live)
-        remap = np.full(len(live), -1, dtype=np.int64)
-        remap[retained] = np.arange(len(retained))
-        for rows in (canonical, terminal):
-            rows[rows >= 0] = remap[rows[rows >= 0]]
-        return OccurrenceState(
-            _gather_one(self.slots, retained), self.owned[torch.from_numpy(retained)], torch.from_numpy(canonical),
-            torch.from_numpy(terminal), self.canonical_positions, self.exact_prefix_len,
-            self.swa_resident[torch.from_numpy(retained)] if self.swa_resident is not None else None)
-
-    def terminal_swa_residency(self):
-        if self.swa_resident is None:
-            return None
-        rows = self.terminal_rows
-        present = rows >= 0
-        result = torch.zeros(len(rows), dtype=torch.bool)
-        result[present] = self.swa_resident[rows[present]]
-        return result
-
-    def live_swa_ranges(self, start: int, end: int):
-        """Raw ``[a, b)`` ranges of ``[start, end)`` whose terminal owner is
-        present (and SWA-resident) -- ``occurrence.py:875-892``."""
-        if end <= start:
-            return []
-        live = np.ones(end - start, dtype=np.bool_)
-        rows = self.terminal_rows[start:end].numpy()
-        present = rows >= 0
-        live[: len(rows)] = present
-        if self.swa_resident is not None:
-            idx = np.flatnonzero(present)
-            live[idx] = self.swa_resident.numpy()[rows[idx]]
-        edges = np.flatnonzero(np.diff(np.concatenate(([0], live.astype(np.int8), [0]))))
-        return [(start + int(a), start + int(b)) for a, b in zip(edges[::2], edges[1::2])]
-
-    def private_slots(self):
-        """Pages the request owns (borrowed pages go back through leases)."""
-        return _gather_one(self.slots, np.flatnonzero(self.owned.numpy()))
-
-    def _nonterminal_private(self):
-        selected = self.owned.numpy().copy()
-        rows = self.terminal_rows.numpy()
-        selected[rows[rows >= 0]] = False
-        return selected
-
-    def nonterminal_private_residency(self):
-        if self.swa_resident is None:
-            return None
-        return self.swa_resident[torch.from_numpy(self._nonterminal_private())]
-
-    def nonterminal_private_slots(self):
-        return _gather_one(self.slots, np.flatnonzero(self._nonterminal_private()))
 
 
 # ---------------------------------------------------------------------------
@@ -595,54 +427,3 @@ def advance_batch(steps):
                          cat([x.copy_destination_slots for x in results]),
                          cat([x.copy_position_pairs for x in results]))
     return results, batch
-
-
-# ---------------------------------------------------------------------------
-# Release.
-
-
-def free_context_slots(allocator, slots, swa_resident=None):
-    """Release private owners, SWA-valid ones through ``free`` and the rest
-    through ``free_full`` (``occurrence.py:936-964``)."""
-    if swa_resident is None:
-        allocator.free(slots)
-        return
-    if swa_resident.device.type != "cpu" or swa_resident.dtype != torch.bool or swa_resident.shape != slots.shape:
-        raise ValueError("Context free SWA metadata must cover the owner slots")
-    if len(slots) == 0:
-        return
-    valid = swa_resident.numpy()
-    if valid.all():
-        allocator.free(slots)
-    elif not valid.any():
-        allocator.free_full(slots)
-    else:
-        live, dead = np.flatnonzero(valid), np.flatnonzero(~valid)
-        allocator.free(_gather_one(slots, live))
-        allocator.free_full(_gather_one(slots, dead))
-
-
-@dataclass
-class ContextPrefillCompletion:
-    """Receipt of a prefill batch; ``complete`` after its completion event
-    (``occurrence.py:967-996``).  ``usage`` records read / repositioned
-    cache statistics (``record_prefill``) and says whether it is recomputing."""
-
-    retired_slots: torch.Tensor
-    usage: object
-    read_cached: torch.Tensor
-    repositioned_cached: torch.Tensor
-    query_count: int
-    completed: bool = False
-    retired_swa_resident: torch.Tensor | None = None
-
-    def __post_init__(self):
-        self.initial_match = not self.usage.recomputing
-
-    def complete(self, allocator):
-        if self.completed:
-            return
-        self.usage.record_prefill(self.read_cached, self.repositioned_cached, self.query_count,
-                                  initial_match=self.initial_match)
-        free_context_slots(allocator, self.retired_slots, self.retired_swa_resident)
-        self.completed = True

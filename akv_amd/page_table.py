@@ -33,9 +33,21 @@ def _idx(t, name):
     return t.data_ptr(), code
 
 
+def _status_ptr(status, device):
+    if status is None:
+        return None
+    if status.dtype != torch.int32 or status.numel() < 1 or status.device != device:
+        raise ValueError("status must be an int32 device word on the output's device")
+    return status.data_ptr()
+
+
 def context_decode_indices(registry, table, rows, lengths, indptr, output, *, starts=None,
-                           mapping=None, multiplier=1):
-    """``out[indptr[b] + i] = T(row[raw])`` over ``len(lengths)`` requests."""
+                           mapping=None, multiplier=1, status=None):
+    """``out[indptr[b] + i] = T(row[raw])`` over ``len(lengths)`` requests.
+
+    ``status``: the compaction's device status word when the registry rows
+    point at its decode layout; the kernel then skips its reads and writes
+    on the device when that compaction's outputs are unusable."""
     if registry.dtype != torch.int64 or registry.ndim != 2 or registry.shape[1] != 6:
         raise ValueError("registry must be int64 [rows, 6]")
     if table.dtype != torch.int32 or table.stride(-1) != 1:
@@ -51,7 +63,7 @@ def context_decode_indices(registry, table, rows, lengths, indptr, output, *, st
         rc = _lib.load().akv_decode_indices(
             registry.data_ptr(), table.data_ptr(), table.stride(0), rows_p, rows_t, len_p, len_t,
             ind_p, ind_t, out_p, out_t, st_p, st_t, map_p, map_t, int(multiplier), len(lengths),
-            current_stream_handle(device),
+            _status_ptr(status, device), current_stream_handle(device),
         )
     _lib.check(rc, "akv_decode_indices")
 

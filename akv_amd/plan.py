@@ -8,7 +8,7 @@ passes run in ``akv_plan_count`` / ``akv_plan_compile`` of ``libakv_amd.so``
 """
 
 import time
-from dataclasses import dataclass, replace
+from dataclasses import dataclass
 
 import torch
 
@@ -207,41 +207,4 @@ def compile_context_layout(
         ignored_repositions=ignored,
         next_position=int(status[3]),
         compile_ns=time.perf_counter_ns() - started,
-    )
-
-
-def append_generated_layout(layout: ContextLayout, token_ids) -> ContextLayout:
-    """Extend a prompt layout with generated tokens at its final stage.
-
-    Mirrors ``append_generated_layout``
-    (``akv/system/sglang/srt/context_system/ir.py:67-104``): generated tokens
-    are born at consecutive positions from ``next_position`` without replaying
-    any event.
-    """
-    tokens = torch.as_tensor(token_ids, dtype=torch.int64, device="cpu")
-    if tokens.ndim != 1 or bool(torch.any((tokens < 0) | (tokens >= 2**31))):
-        raise ValueError("Generated Context IDs must be an int32 token vector")
-    count = len(tokens)
-    if not count:
-        return layout
-    if layout.next_position + count > 2**31 - 1:
-        raise ValueError("Generated Context positions exceed int32 range")
-    n, record_count = len(layout.positions), len(layout.records)
-    positions = torch.arange(layout.next_position, layout.next_position + count, dtype=torch.int32)
-    stages = torch.full((count,), len(layout.transition_offsets) - 1, dtype=torch.int32)
-    records = torch.stack((torch.zeros_like(positions), tokens.int(), positions), 1)
-    return replace(
-        layout,
-        records=torch.cat((layout.records, records)),
-        virtual_mask=torch.cat((layout.virtual_mask, torch.zeros(count, dtype=torch.bool))),
-        key_to_token=torch.cat((layout.key_to_token, torch.arange(n, n + count))),
-        token_to_key=torch.cat(
-            (layout.token_to_key, torch.arange(record_count, record_count + count))
-        ),
-        positions=torch.cat((layout.positions, positions)),
-        keep_mask=torch.cat((layout.keep_mask, torch.ones(count, dtype=torch.bool))),
-        materialized_stage=torch.cat((layout.materialized_stage, stages)),
-        birth_positions=torch.cat((layout.birth_positions, positions)),
-        birth_stages=torch.cat((layout.birth_stages, stages)),
-        next_position=layout.next_position + count,
     )

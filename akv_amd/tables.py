@@ -140,7 +140,9 @@ def allocate_outputs(inputs, device, *, generated_total=None):
         kv_indptr=indptr,
         last_page_len=None if indptr is None else torch.empty(inputs.n_requests, dtype=i32, device=device),
         counts=torch.empty((inputs.n_requests, 3), dtype=i32, device=device),
-        status=torch.zeros(1, dtype=i32, device=device),
+        # outputs no compaction has written yet are unusable: a gated consumer
+        # launched before the first compaction does nothing
+        status=torch.full((1,), _lib.AKV_STATUS_INCOMPLETE, dtype=i32, device=device),
         workspace=torch.zeros(max(8, (ws_bytes + 7) // 8), dtype=torch.int64, device=device),
     )
 
@@ -218,21 +220,24 @@ def compact_rows(inputs, req_to_token, req_rows, fresh_slots, outputs, *, row_po
 
 
 _STATUS_BITS = (
-    (1, "fresh slot count or an output capacity does not match the batch"),
-    (2, "the one-launch barrier did not complete (workspace not zero-filled before its first use?)"),
-    (4, "a tile stopped waiting at the one-launch barrier (tiles could not all run at once)"),
+    (_lib.AKV_STATUS_SIZES, "fresh slot count or an output capacity does not match the batch"),
+    (_lib.AKV_STATUS_INCOMPLETE, "an output was not written"),
 )
 
 
 def check_status(outputs):
-    """Wait for the compaction and raise if its status word is not 0; its
-    outputs are then partial and must not reach the Reposition or the decode
-    metadata.  Synchronises with the device (one 4-byte read)."""
+    """Host-side check of a finished compaction, for tests and diagnostics:
+    waits for the device (one 4-byte read) and raises when the status word
+    marks the outputs unusable; returns the word (bit
+    ``AKV_STATUS_REBUILT`` only says that the one-pass path's finishing
+    launch rebuilt some tiles).  The hot path never calls it: consumers read
+    the word on the device through their ``status`` argument and skip their
+    work when it is set."""
     code = int(outputs.status.item())
-    if code:
-        why = "; ".join(text for bit, text in _STATUS_BITS if code & bit) or "unknown"
+    if code & _lib.AKV_STATUS_UNUSABLE:
+        why = "; ".join(text for bit, text in _STATUS_BITS if code & bit)
         raise RuntimeError(f"akv_compact_rows status {code}: {why}")
-    return outputs
+    return code
 
 
 # ---------------------------------------------------------------------------

@@ -33,12 +33,14 @@ def _slots(s, n, what):
 
 
 def copy_kv_rows(src_k_ptrs, src_v_ptrs, src_layout, dst_k_ptrs, dst_v_ptrs, dst_layout, n_tokens, *,
-                 src_slots=None, dst_slots=None):
+                 src_slots=None, dst_slots=None, status=None):
     """Copy K and V rows of every layer: ``dst[dst_slots[t]] = src[src_slots[t]]``.
 
     ``*_ptrs``: device uint64/int64 ``[layers]`` base addresses; ``*_layout``:
     an exemplar layer tensor giving the row size and slot stride of that side.
-    A missing slot vector means slot ``t`` (a packed buffer).
+    A missing slot vector means slot ``t`` (a packed buffer).  ``status``:
+    the compaction's device status word when a slot vector comes from it
+    (nothing is copied, on the device, when it reports the lists unusable).
     """
     for p in (src_k_ptrs, src_v_ptrs, dst_k_ptrs, dst_v_ptrs):
         if p.dtype not in (torch.uint64, torch.int64) or p.ndim != 1 or not p.is_contiguous():
@@ -50,13 +52,16 @@ def copy_kv_rows(src_k_ptrs, src_v_ptrs, src_layout, dst_k_ptrs, dst_v_ptrs, dst
     drow, dst_stride = _row_layout(dst_layout)
     if row != drow:
         raise ValueError("source and destination rows differ in size")
+    if status is not None and (status.dtype != torch.int32 or status.numel() < 1
+                               or status.device != src_k_ptrs.device):
+        raise ValueError("status must be an int32 device word on the pointer tables' device")
     lib = _lib.load()
     device = src_k_ptrs.device
     with _on_device(device):
         rc = lib.akv_copy_kv_rows(
             src_k_ptrs.data_ptr(), src_v_ptrs.data_ptr(), dst_k_ptrs.data_ptr(), dst_v_ptrs.data_ptr(), n_layers, row,
             src_stride, src_stride, dst_stride, dst_stride, _slots(src_slots, n_tokens, "src_slots"),
-            _slots(dst_slots, n_tokens, "dst_slots"), int(n_tokens), current_stream_handle(device),
+            _slots(dst_slots, n_tokens, "dst_slots"), int(n_tokens), _lib.ptr(status), current_stream_handle(device),
         )
     _lib.check(rc, "akv_copy_kv_rows")
 

@@ -5,11 +5,13 @@ Workload: one GPT-OSS-120B-shaped request (36 layers, 8 KV heads, head_dim
 page size 1) of 32768 tokens dropping 12 seeded spans (~40%), then one
 Reposition.  Synthetic data; all inputs resident in HBM before timing.
 
-One step = the whole GPU side of the hot path: page-table compaction
-(terminal row, freed slots, copy lists, decode layout, kv_indptr /
-kv_indices; 2 kernels) -> all-layer Reposition (K re-rotation + V move, one
-launch).  ``value`` = retained-KV bytes moved (K and V, read + write) per
-step / step time over K back-to-back steps.  Also reported: the Reposition
+One step = the whole GPU side of the hot path as a caller runs it:
+page-table compaction (terminal row, freed slots, copy lists, decode layout,
+kv_indptr / kv_indices; 2 launches) -> all-layer Reposition (K re-rotation +
+V move, one launch) gated on the device by the compaction's status word.  No
+host read or sync sits between them, in the product or here.  ``value`` =
+retained-KV bytes moved (K and V, read + write) per step / step time over K
+back-to-back steps.  Also reported: the Reposition
 kernel's average launch in that timed region and its roofline against
 8 TB/s; p50 / p99 latency of the step and of the Reposition alone after a
 1 GiB read flush of L2 + the 256 MB MALL; the CPU oracle on a bounded sample
@@ -18,15 +20,13 @@ their own workloads: the tiny and ragged-batch compactions, ascending slots,
 one TP=2 rank's head share,
 the decode step over the compacted metadata, the next turn's prefill
 attention (GPT-OSS and Llama-3 layer shapes), a multi-turn trajectory's
-occurrence binding in one forward and in 4 chunked forwards with cache
-publication, the compacted handoff copies and the page-16 copy-on-write
-batch.
+occurrence binding in one forward and in 4 chunked forwards, the
+compacted handoff copies and the page-16 copy-on-write batch.
 """
 
 import argparse
 import json
 import os
-import subprocess
 import sys
 import time
 from pathlib import Path
@@ -75,6 +75,7 @@ def copy_calibration(device):
 class Pipeline:
     def __init__(self, name, device, slot_order="permutation"):
         self.device = device
+        self.w_name = name
         w = self.w = synth.workload(name)
         if w.n_requests != 1:
             raise SystemExit("the bench workload must be a single request")
@@ -110,25 +111,25 @@ class Pipeline:
         kv_bytes = 2  # bf16
         self.retained_bytes = self.moved * 4 * m.n_layers * m.n_heads * m.head_dim * kv_bytes
         self.alg_bytes = self.retained_bytes + self.moved * 16 + self.moved * 2 * m.rotary_dim * 4
-        self.checked_compaction()
+        # the lists exist from construction on (a gated Reposition of outputs
+        # no compaction wrote would do nothing; an ungated one would read
+        # uninitialised slots)
+        self.compaction()
 
     def compaction(self):
         tables.compact_rows(self.inputs, self.table, self.rows, self.fresh, self.out, generated=self.generated,
                             birth_slots=self.birth)
 
     def reposition(self):
+        # gated on the device by the compaction's status word: the lists go
+        # from the compaction to the Reposition with no host read
         p, o = self.pool, self.out
-        ops.reposition_kv_layers(p.k_ptrs, p.v_ptrs, p.k[0], p.v[0], o.copy_src, o.copy_dst, o.copy_pairs,
-                                 self.rope, is_neox_style=self.w.model.is_neox_style)
+        ops.reposition_kv_layers_gated(p.k_ptrs, p.v_ptrs, p.k[0], p.v[0], o.copy_src, o.copy_dst, o.copy_pairs,
+                                       self.rope, status=o.status, is_neox_style=self.w.model.is_neox_style)
 
     def step(self):
         self.compaction()
         self.reposition()
-
-    def checked_compaction(self):
-        # once, before any timed step: a failed compaction must not feed the Reposition
-        self.compaction()
-        tables.check_status(self.out)
 
     def flush(self):
         # read 1 GiB: evicts the MALL and L2 with clean lines, so the timed
@@ -270,10 +271,9 @@ def ragged_config(device, flush):
     def step():
         tables.compact_rows(inputs, table, rows, fresh, out, generated=gen, birth_slots=birth)
 
-    step()
-    tables.check_status(out)
     warm, cold = _time_steps(step, 50, 10, 50, flush)
     graph = _graph_steps(step, 50)
+    status = tables.check_status(out)  # after timing: the outputs were complete
     total = sum(w.lengths)
     # bytes: keep + positions + birth slot read, row write, lists written
     meta = total * (1 + 8 + 4 + 4) + 4 * inputs.retired_total + 16 * inputs.moved_total \
@@ -283,8 +283,8 @@ def ragged_config(device, flush):
         "moved": inputs.moved_total, "step_ms_back_to_back": round(warm, 5),
         "step_ms_graph_replay": round(graph, 5),
         "step_p50_ms": round(percentile(cold, 50), 5), "step_p99_ms": round(percentile(cold, 99), 5),
-        "kernel_launches_per_step": compaction_launches(inputs),
-        "metadata_bytes": meta, "host_event_compile_ms": round(compile_ms, 1),
+        "kernel_launches_per_step": compaction_launches(inputs), "compaction_passes": compaction_passes(inputs),
+        "status": status, "metadata_bytes": meta, "host_event_compile_ms": round(compile_ms, 1),
     }
 
 
@@ -311,7 +311,6 @@ def decode_consumer_config(device, flush):
     tables.compact_rows(inputs, table, rows, torch.from_numpy(np.concatenate(slots.fresh)).to(device), out,
                         generated=torch.ones(B, dtype=torch.int32, device=device),
                         birth_slots=torch.from_numpy(np.concatenate(slots.birth_rows)).to(device))
-    tables.check_status(out)
     pool = synth.make_pool(model, w.pool_slots, device, seed=9, generate_on_device=True)
 
     # registry rows (the reference registry's row format) straight from the
@@ -329,7 +328,8 @@ def decode_consumer_config(device, flush):
     def meta_window():
         page_table.context_window_lengths(registry, rows, seq, win_len, 128, starts=win_start)
         page_table.build_indptr(win_len, win_indptr)
-        page_table.context_decode_indices(registry, table, rows, win_len, win_indptr, win_idx, starts=win_start)
+        page_table.context_decode_indices(registry, table, rows, win_len, win_indptr, win_idx, starts=win_start,
+                                          status=out.status)
 
     meta_window()
     q = torch.randn((B, 64, 64), device=device).to(torch.bfloat16)
@@ -340,11 +340,11 @@ def decode_consumer_config(device, flush):
 
     def full():
         attention.decode_attention(q, pool.k[1], pool.v[1], out.kv_indptr, out.kv_indices, o, scale=0.125,
-                                   max_len=max_full, sinks=sinks, workspace=ws)
+                                   max_len=max_full, sinks=sinks, workspace=ws, status=out.status)
 
     def windowed():
         attention.decode_attention(q, pool.k[0], pool.v[0], win_indptr, win_idx, o, scale=0.125, max_len=129,
-                                   sinks=sinks, workspace=ws)
+                                   sinks=sinks, workspace=ws, status=out.status)
 
     # the step's own read metadata from the registry: kv_indptr + kv_indices
     # for the full layer, window lengths + indptr + indices for the SWA layer
@@ -353,9 +353,10 @@ def decode_consumer_config(device, flush):
 
     def meta_full():
         page_table.build_indptr(seq, meta_indptr)
-        page_table.context_decode_indices(registry, table, rows, seq, meta_indptr, meta_idx)
+        page_table.context_decode_indices(registry, table, rows, seq, meta_indptr, meta_idx, status=out.status)
 
     meta_full()
+    tables.check_status(out)  # a check of this run, after the gated consumers
     if not (torch.equal(meta_indptr, out.kv_indptr.to(torch.int32)) and torch.equal(meta_idx, out.kv_indices)):
         raise RuntimeError("decode read indices disagree with the compaction's kv_indices")
     warm_meta_full, cold_meta_full = _time_steps(meta_full, 50, 5, 20, flush)
@@ -521,23 +522,39 @@ def multistage_config(device, flush):
 CHUNKS = 4
 
 
+def _published_terminals(state, layout, query_end):
+    """Raw tokens [0, query_end) whose terminal versions the forward ending at
+    query_end binds (the scheduler's choice, an input of the plan): kept
+    tokens that have an owner to bind from -- every token new in this
+    forward does, an earlier one needs a canonical or terminal row -- and,
+    before the last forward, only those already at their final position."""
+    start = len(state.canonical_rows)
+    final = np.asarray(layout.positions[:query_end])
+    kept = np.asarray(layout.keep_mask[:query_end], dtype=bool)
+    terminal = state.terminal_rows.numpy() >= 0
+    owner = np.concatenate(((state.canonical_rows.numpy() >= 0) | terminal, np.ones(query_end - start, bool)))
+    if query_end == len(layout.positions):
+        return torch.from_numpy(kept & owner)
+    ready = np.concatenate(((state.canonical_positions.numpy() == final[:start]) | terminal,
+                            np.asarray(layout.birth_positions[start:query_end]) == final[start:]))
+    return torch.from_numpy(kept & owner & ready)
+
+
 def _chunked_lifecycle(device, lay, visible, n, chunks, slot_perm, on_copies=None, timings=None):
-    """One request prefilled in ``chunks`` forwards with per-chunk cache
-    publication: window (C++), plan (C++), slot allocation, advance (C++ +
-    one gather launch), the chunk's Reposition (``on_copies``), publication
-    (one gather launch).  Returns the final state."""
+    """One request prefilled in ``chunks`` forwards: window (C++), plan
+    (C++), slot allocation, advance (C++ + one gather launch), the chunk's
+    Reposition (``on_copies``).  Returns the final state."""
     from akv_amd import occurrence as ow
     from akv_amd import ownership as own
 
-    state = own.OccurrenceState.from_match(torch.empty(0, dtype=torch.int64, device=device),
-                                           torch.empty(0, dtype=torch.int32), exact_prefix_len=0)
+    state = own.OccurrenceState.empty(device)
     next_slot = 0
     bounds = np.linspace(0, n, chunks + 1).astype(int)
     for qs, qe in zip(bounds[:-1], bounds[1:]):
         t0 = time.perf_counter()
         window = ow.compile_occurrence_window(lay, visible, lay.positions, query_start=int(qs), query_end=int(qe))
         t1 = time.perf_counter()
-        plan = state.plan(window, state.prefill_terminal_keep(lay, int(qe)))
+        plan = state.plan(window, _published_terminals(state, lay, int(qe)))
         t2 = time.perf_counter()
         q = slot_perm[next_slot : next_slot + qe - qs]
         extra = slot_perm[next_slot + qe - qs : next_slot + qe - qs + plan.extra_page_count]
@@ -547,22 +564,17 @@ def _chunked_lifecycle(device, lay, visible, n, chunks, slot_perm, on_copies=Non
         if on_copies is not None:
             on_copies(adv)
         state = adv.state
-        t4 = time.perf_counter()
-        if qe < n:
-            state = state.publish(state.terminal_slots(), cache_len=int(qe))
-        t5 = time.perf_counter()
         if timings is not None:
-            timings.append(dict(window=t1 - t0, plan=t2 - t1, advance=t3 - t2, publish=t5 - t4,
-                                copies=int(plan.extra_page_count), occurrences=window.occurrence_count))
+            timings.append(dict(window=t1 - t0, plan=t2 - t1, advance=t3 - t2, copies=int(plan.extra_page_count),
+                                occurrences=window.occurrence_count))
     return state
 
 
 def chunked_config(device, flush):
     """The same 6-turn 32768-token trajectory prefilled in 4 chunks of 8192
-    with per-chunk cache publication (chunked prefill over the radix cache):
-    per chunk the host window / plan / advance (C++), one gather launch for
-    every slot list of the forward, the Reposition of its copies and one
-    gather launch for the publication."""
+    (chunked prefill): per chunk the host window / plan / advance (C++), one
+    gather launch for every slot list of the forward and the Reposition of
+    its copies."""
     from akv_amd import plan as lp
 
     n = 32768
@@ -608,14 +620,13 @@ def chunked_config(device, flush):
     torch.cuda.empty_cache()
     ms = lambda key: [round(t[key] * 1e3, 3) for t in timings]
     return {
-        "workload": f"gpt-oss-120b 6-turn trajectory, {n} tokens, {CHUNKS} chunked forwards with cache publication",
+        "workload": f"gpt-oss-120b 6-turn trajectory, {n} tokens, {CHUNKS} chunked forwards",
         "kept": kept, "copies_per_chunk": ncopies, "occurrences_per_chunk": [t["occurrences"] for t in timings],
-        "host_window_ms": ms("window"), "host_plan_ms": ms("plan"),
-        "advance_ms": ms("advance"), "publish_ms": ms("publish"),
+        "host_window_ms": ms("window"), "host_plan_ms": ms("plan"), "advance_ms": ms("advance"),
         "reposition_ms": [round(x, 4) for x in repo],
         "reposition_pct_hbm_peak": round(100 * alg / (sum(repo) / 1e3) / 1e9 / HBM_PEAK_GBS, 2) if repo else None,
         "request_wall_ms": round(wall * 1e3, 2),
-        "kernel_launches_per_chunk": {"advance gather": 1, "reposition": 1, "publish gather": 2},
+        "kernel_launches_per_chunk": {"advance gather": 1, "reposition": 1},
     }
 
 
@@ -728,33 +739,47 @@ def prefill_llama_config(device, flush, extend=4096):
 CEILING_ROUNDS = 3
 
 
-def ceiling_legs(pipe, steps, warmup, flush):
-    """Ceilings of the Reposition's access pattern, timed in the same run.
+def _alternating(legs, steps, warmup, flush):
+    """Median launch time of each leg over CEILING_ROUNDS rounds, the legs
+    taking turns within every round (none always runs first after other
+    work)."""
+    times = {name: [] for name in legs}
+    for _ in range(CEILING_ROUNDS):
+        for name, fn in legs.items():
+            times[name].append(_time_steps(fn, steps, warmup, 0, flush)[0])
+    return {name: float(np.median(v)) for name, v in times.items()}
 
-    * gather copy: ``akv_copy_kv_rows`` of the same source -> destination K
-      and V rows of every layer (no arithmetic, one launch), in the order the
-      copy lists hold (raw token order), sorted by source slot and sorted by
-      destination slot;
-    * streaming copy: the same kernel between two packed buffers of the same
-      byte count (no slot lists: consecutive rows);
-    * the Reposition itself with its lists permuted into the same two sorted
-      orders (its output does not depend on the order: destinations are
-      disjoint).
-    Each pair is timed in CEILING_ROUNDS alternating rounds (gather, then
-    Reposition) and each reports the median round.
-    Rates: K/V bytes read + written per launch / average launch time; the
-    Reposition's rate counts its algorithmic bytes (slot lists and table rows
-    as well), as ``roofline.achieved`` does."""
+
+def _torch_rows_legs(pipe, steps, warmup, flush):
+    """The moved K/V rows through kernels not written here: torch's
+    index_select (rows gathered into a packed tensor) and index_copy_
+    (scattered back), over one int16 [2 x layers, slots, row] tensor so that
+    each is a single launch over every layer.  Rates count the rows' bytes
+    read and written by each launch."""
+    m, o = pipe.w.model, pipe.out
+    n, layers = pipe.moved, 2 * m.n_layers
+    row = m.n_heads * m.head_dim
+    big = torch.empty((layers, pipe.w.pool_slots, row), dtype=torch.int16, device=pipe.device)
+    big.random_(-1000, 1000)
+    src, dst = o.copy_src.long(), o.copy_dst.long()
+    tmp = torch.empty((layers, n, row), dtype=torch.int16, device=pipe.device)
+    nbytes = 2 * n * layers * row * 2
+    ms = _alternating({"select": lambda: torch.index_select(big, 1, src, out=tmp),
+                       "copy": lambda: big.index_copy_(1, dst, tmp)}, steps, warmup, flush)
+    del big, tmp
+    torch.cuda.empty_cache()
+    return {"index_select_GBs": round(nbytes / (ms["select"] / 1e3) / 1e9, 1),
+            "index_copy_GBs": round(nbytes / (ms["copy"] / 1e3) / 1e9, 1)}
+
+
+def _gather_legs(pipe, steps, warmup, flush, orders):
+    """akv_copy_kv_rows of the pipeline's src -> dst rows beside its
+    Reposition, in the given list orders (the Reposition's output does not
+    depend on the order: destinations are disjoint)."""
     from akv_amd import transfer
 
     o, p, m = pipe.out, pipe.pool, pipe.w.model
     n = pipe.moved
-    kv_bytes = pipe.retained_bytes
-
-    def rate(ms, nbytes):
-        return round(nbytes / (ms / 1e3) / 1e9, 1)
-
-    orders = {"raw": None, "by_source_slot": torch.argsort(o.copy_src), "by_destination_slot": torch.argsort(o.copy_dst)}
     out = {"gather_copy_GBs": {}, "reposition_GBs": {}}
     for name, perm in orders.items():
         src = o.copy_src if perm is None else o.copy_src[perm].contiguous()
@@ -769,29 +794,89 @@ def ceiling_legs(pipe, steps, warmup, flush):
             ops.reposition_kv_layers(p.k_ptrs, p.v_ptrs, p.k[0], p.v[0], src, dst, pairs, pipe.rope,
                                      is_neox_style=m.is_neox_style)
 
-        # alternating rounds, the median of each: neither kernel always runs
-        # first after other work
-        g_ms, r_ms = [], []
-        for _ in range(CEILING_ROUNDS):
-            g_ms.append(_time_steps(gather, steps, warmup, 0, flush)[0])
-            r_ms.append(_time_steps(repo, steps, warmup, 0, flush)[0])
-        out["gather_copy_GBs"][name] = rate(float(np.median(g_ms)), kv_bytes)
-        out["reposition_GBs"][name] = rate(float(np.median(r_ms)), pipe.alg_bytes)
+        ms = _alternating({"gather": gather, "repo": repo}, steps, warmup, flush)
+        out["gather_copy_GBs"][name] = round(pipe.retained_bytes / (ms["gather"] / 1e3) / 1e9, 1)
+        out["reposition_GBs"][name] = round(pipe.alg_bytes / (ms["repo"] / 1e3) / 1e9, 1)
+    return out
+
+
+def _streaming_leg(pipe, steps, warmup, flush):
+    from akv_amd import transfer
+
+    m, n = pipe.w.model, pipe.moved
     a = transfer.PackedKV.empty(m.n_layers, n, m.n_heads, m.head_dim, m.dtype, pipe.device)
     b = transfer.PackedKV.empty(m.n_layers, n, m.n_heads, m.head_dim, m.dtype, pipe.device)
     a.k.fill_(1.0)
     a.v.fill_(1.0)
-
-    def stream():
-        transfer.copy_kv_rows(a.k_ptrs, a.v_ptrs, a.k[0], b.k_ptrs, b.v_ptrs, b.k[0], n)
-
-    warm, _ = _time_steps(stream, steps, warmup, 0, flush)
-    out["streaming_copy_GBs"] = rate(warm, kv_bytes)
+    warm, _ = _time_steps(lambda: transfer.copy_kv_rows(a.k_ptrs, a.v_ptrs, a.k[0], b.k_ptrs, b.v_ptrs, b.k[0], n),
+                          steps, warmup, 0, flush)
     del a, b
     torch.cuda.empty_cache()
-    out["reposition_frac_of_gather"] = round(out["reposition_GBs"]["raw"] / out["gather_copy_GBs"]["raw"], 4)
-    out["reposition_frac_of_streaming"] = round(out["reposition_GBs"]["raw"] / out["streaming_copy_GBs"], 4)
-    out["kernel"] = "akv_copy_kv_rows (layer-major, one 1 KiB row per wave)"
+    return round(pipe.retained_bytes / (warm / 1e3) / 1e9, 1)
+
+
+def _row_size_legs(pipe, steps, warmup, flush):
+    """The same random src -> dst lists over pools of 4 and 16 KV heads
+    (512 B and 2 KiB rows): does the random pattern's ceiling move with the
+    row size?"""
+    import dataclasses
+
+    from akv_amd import transfer
+
+    o, m, n = pipe.out, pipe.w.model, pipe.moved
+    out = {}
+    for heads in (4, 16):
+        model = dataclasses.replace(m, n_heads=heads)
+        pool = synth.make_pool(model, pipe.w.pool_slots, pipe.device, seed=3, generate_on_device=True)
+        nbytes = n * 4 * m.n_layers * heads * m.head_dim * 2
+        warm, _ = _time_steps(lambda: transfer.copy_kv_rows(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.k_ptrs,
+                                                            pool.v_ptrs, pool.k[0], n, src_slots=o.copy_src,
+                                                            dst_slots=o.copy_dst), steps, warmup, 0, flush)
+        out[f"{heads * m.head_dim * 2}B"] = round(nbytes / (warm / 1e3) / 1e9, 1)
+        del pool
+        torch.cuda.empty_cache()
+    return out
+
+
+def ceiling_legs(pipe, steps, warmup, flush):
+    """Ceilings of the Reposition's access pattern, timed in the same run.
+
+    Random slots (the workload's own lists):
+    * gather copy: ``akv_copy_kv_rows`` of the same source -> destination K
+      and V rows of every layer (no arithmetic, one launch), in raw order,
+      sorted by source slot and sorted by destination slot, each beside the
+      Reposition with its lists in the same order;
+    * torch's ``index_select`` / ``index_copy_`` over the same rows (kernels
+      not written here);
+    * the gather at 512 B and 2 KiB rows (the same lists over 4- and 16-head
+      pools);
+    * streaming copy: the same byte count between two packed buffers.
+    Ascending slots (the same request, slots from an unfragmented free list):
+    the gather, the Reposition, torch's pair and the streaming copy.
+    Rates: K/V bytes read + written per launch / average launch time; the
+    Reposition's rate counts its algorithmic bytes (slot lists and table rows
+    as well), as ``roofline.achieved`` does."""
+    o = pipe.out
+    orders = {"raw": None, "by_source_slot": torch.argsort(o.copy_src), "by_destination_slot": torch.argsort(o.copy_dst)}
+    out = {"random": _gather_legs(pipe, steps, warmup, flush, orders)}
+    r = out["random"]
+    r["torch"] = _torch_rows_legs(pipe, steps, warmup, flush)
+    r["gather_copy_by_row_size_GBs"] = _row_size_legs(pipe, steps, warmup, flush)
+    r["streaming_copy_GBs"] = _streaming_leg(pipe, steps, warmup, flush)
+    r["reposition_frac_of_gather"] = round(r["reposition_GBs"]["raw"] / r["gather_copy_GBs"]["raw"], 4)
+    r["reposition_frac_of_streaming"] = round(r["reposition_GBs"]["raw"] / r["streaming_copy_GBs"], 4)
+    asc = Pipeline(pipe.w_name, pipe.device, slot_order="ascending")
+    asc.compaction()
+    a = out["ascending"] = _gather_legs(asc, steps, warmup, flush, {"raw": None})
+    a["torch"] = _torch_rows_legs(asc, steps, warmup, flush)
+    a["streaming_copy_GBs"] = _streaming_leg(asc, steps, warmup, flush)
+    a["reposition_frac_of_gather"] = round(a["reposition_GBs"]["raw"] / a["gather_copy_GBs"]["raw"], 4)
+    del asc
+    torch.cuda.empty_cache()
+    best = max([v for v in r["gather_copy_GBs"].values()] + list(r["torch"].values())
+               + list(r["gather_copy_by_row_size_GBs"].values()))
+    out["best_random_row_copy_pct_hbm_peak"] = round(100 * best / HBM_PEAK_GBS, 2)
+    out["kernel"] = "akv_copy_kv_rows (layer-major, one row per wave); torch index_select / index_copy_"
     out["rounds"] = CEILING_ROUNDS
     return out
 
@@ -881,8 +966,8 @@ def cpu_baseline(pipe, runs):
         "runs": runs,
         "bit_exact_vs_gpu": exact,
         "chunked_ownership_ms": round(chunked_s * 1e3, 1),
-        "chunked_ownership_sample": (f"numpy oracle of the chunked-prefill ownership (window, plan, advance, "
-                                     f"publication; {CHUNKS} chunks of the 32768-token trajectory), host time"),
+        "chunked_ownership_sample": (f"numpy oracle of the chunked-prefill ownership (window, plan, advance; "
+                                     f"{CHUNKS} chunks of the 32768-token trajectory), host time"),
         "host": host_info(threads),
     }
 
@@ -910,38 +995,48 @@ def _chunked_ownership_port():
         extra = slots[used + qe - qs : used + qe - qs + p["extra_page_count"]]
         used += qe - qs + p["extra_page_count"]
         st = st.advance(win, p, q, extra, visible).state
-        if qe < n:
-            st = st.publish(st.terminal_slots(), cache_len=int(qe))
     return time.perf_counter() - t0
 
 
-def compaction_launches(inputs):
-    """Kernel launches akv_compact_rows makes for this batch on this device."""
+def compaction_passes(inputs):
+    """Passes akv_compact_rows makes over this batch on this device: 1 (one
+    kernel whose tiles meet at an in-kernel barrier) or 2 (count, scatter)."""
     total = sum(inputs.n_tokens)
     return int(_lib.load().akv_compact_launches(inputs.n_requests, total, total + inputs.n_requests, None))
 
 
+def compaction_launches(inputs):
+    """Kernel launches of akv_compact_rows: two on either path (the one-pass
+    kernel and its one-workgroup finishing launch, or count and scatter)."""
+    return 2 if compaction_passes(inputs) else 0
+
+
 def host_info(threads):
-    """lscpu model name and core counts of this host."""
-    info = {}
+    """CPU model and core counts of this host, read from /proc/cpuinfo (no
+    child process is started from the GPU process)."""
+    fields, physical = {}, set()
     try:
-        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
-        for line in out.splitlines():
-            key, _, val = line.partition(":")
-            info[key.strip()] = val.strip()
-    except (OSError, subprocess.SubprocessError):
+        with open("/proc/cpuinfo") as f:
+            block = {}
+            for line in f.read().splitlines() + [""]:
+                if not line.strip():
+                    if block:
+                        for key in ("model name", "vendor_id", "cpu family", "model", "stepping"):
+                            fields.setdefault(key, block.get(key, ""))
+                        physical.add((block.get("physical id", "0"), block.get("core id", block.get("processor"))))
+                    block = {}
+                    continue
+                key, _, val = line.partition(":")
+                block[key.strip()] = val.strip()
+    except OSError:
         pass
-    cores_per_socket = int(info.get("Core(s) per socket", "0") or 0)
-    sockets = int(info.get("Socket(s)", "0") or 0)
-    # a virtual machine may report only the vendor line as the model name:
-    # the family / model / stepping numbers identify the part
-    family = info.get("CPU family", "?")
-    return {"cpu": info.get("Model name", ""),
-            "cpu_family_model_stepping": "/".join(info.get(k, "?") for k in ("CPU family", "Model", "Stepping")),
+    family = fields.get("cpu family", "?")
+    return {"cpu": fields.get("model name", ""),
+            "cpu_family_model_stepping": "/".join(fields.get(k, "?") for k in ("cpu family", "model", "stepping")),
             # AMD family 26 (1Ah) is the Zen 5 core of the EPYC 9005 series
-            "cpu_core_generation": "Zen 5 (EPYC 9005 series)" if family == "26" and "AMD" in info.get(
-                "Vendor ID", "") + info.get("Model name", "") else None,
-            "physical_cores": cores_per_socket * sockets or None,
+            "cpu_core_generation": "Zen 5 (EPYC 9005 series)" if family == "26" and "AMD" in fields.get(
+                "vendor_id", "") + fields.get("model name", "") else None,
+            "physical_cores": len(physical) or None,
             "logical_cpus": os.cpu_count(), "cpus_available": len(os.sched_getaffinity(0)),
             "torch_threads": threads}
 
@@ -1022,6 +1117,9 @@ def main():
         step_ms.append(e0.elapsed_time(e2))
         repo_ms.append(e1.elapsed_time(e2))
     print(f"# latency iterations done: {args.latency_iters}", file=sys.stderr, flush=True)
+    # a check of this run (after every timed step, not between compaction and
+    # Reposition): the lists were complete
+    status = None if args.reposition_only else tables.check_status(pipe.out)
 
     # the same launch with every pair at its birth position: a pure row copy
     # of the same slots (same bytes, no rotation) -- the access pattern's own
@@ -1084,9 +1182,12 @@ def main():
         # the access pattern's own ceilings, same run (see ceiling_legs)
         "ceiling": ceiling,
         "pct_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
-        # compaction: count + scatter; Reposition: one launch for the
-        # 36-layer group
+        # compaction: two launches (one pass + its finishing workgroup);
+        # Reposition: one launch for the 36-layer group, gated on the device
+        # by the compaction's status word
         "kernel_launches_per_step": 1 if args.reposition_only else compaction_launches(pipe.inputs) + 1,
+        "compaction_passes": None if args.reposition_only else compaction_passes(pipe.inputs),
+        "compaction_status": status,
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),

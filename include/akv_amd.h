@@ -38,6 +38,26 @@ extern "C" {
 #define AKV_I32 0
 #define AKV_I64 1
 
+/*
+ * Bits of the status word akv_compact_rows writes (int32, device memory).
+ * Once the call's launches have run: 0 = the outputs are complete and
+ * usable; AKV_STATUS_SIZES = fresh_count or an output capacity does not
+ * match the batch (lists truncated or partly unwritten); AKV_STATUS_INCOMPLETE
+ * = an output was not written (set while the one-launch kernel runs, never
+ * left set once its finishing launch has run); AKV_STATUS_REBUILT = the
+ * one-launch kernel's tiles could not all meet at its barrier and the
+ * finishing launch rebuilt their outputs (informational: the outputs are
+ * complete).  Consumers that take a `status` pointer (the gated Reposition,
+ * akv_decode_indices, akv_decode_attention*, akv_copy_kv_rows) read the word
+ * on the device and, when (*status & AKV_STATUS_UNUSABLE) != 0, write
+ * nothing and read no K/V row or table entry through the lists, so the
+ * compaction's outputs can be handed on with no host read or sync.
+ */
+#define AKV_STATUS_SIZES 1
+#define AKV_STATUS_INCOMPLETE 2
+#define AKV_STATUS_REBUILT 4
+#define AKV_STATUS_UNUSABLE (AKV_STATUS_SIZES | AKV_STATUS_INCOMPLETE)
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* akv_last_error(void);
 
@@ -70,23 +90,52 @@ int akv_reposition_kv_layers(const uint64_t* k_ptrs, const uint64_t* v_ptrs,
                              int32_t skip_unmapped, void* stream);
 
 /*
+ * akv_reposition_kv_layers gated by the status word of the akv_compact_rows
+ * call that wrote src / dst / pairs: when status is not NULL and
+ * (*status & AKV_STATUS_UNUSABLE) != 0 on the device, no list entry is
+ * dereferenced and nothing is written.  The word is read by every
+ * workgroup, so the lists go from the compaction to the Reposition on one
+ * stream with no host read.  status NULL = akv_reposition_kv_layers.
+ * Same kernels and arguments as akv_reposition_kv_layers, whose signature
+ * the reference's callers keep.  The gate is what the reference's "no
+ * GPU-to-CPU reads and no synchronization" contract needs once the lists
+ * are built on the device
+ * (akv/system/sglang/kernels/ops/attention/context_reposition.py:148-151).
+ */
+int akv_reposition_kv_layers_gated(const uint64_t* k_ptrs, const uint64_t* v_ptrs,
+                                   int32_t n_layers, int32_t kv_dtype,
+                                   int32_t n_heads, int32_t head_dim,
+                                   int32_t rotary_dim, int64_t k_stride_slot,
+                                   int64_t k_stride_head, int64_t v_stride_slot,
+                                   int64_t v_stride_head, const int32_t* src,
+                                   const int32_t* dst, const int32_t* pairs,
+                                   int64_t pair_stride, int64_t n_tokens,
+                                   const void* cos_sin, int32_t cos_sin_dtype,
+                                   int64_t rope_stride, int32_t is_neox,
+                                   int32_t skip_unmapped, const int32_t* status,
+                                   void* stream);
+
+/*
  * Device bytes of the workspace akv_compact_rows needs for a batch of
  * n_requests holding total_tokens raw tokens in all (16-byte aligned).  The
- * workspace must be zero-filled once before its first use; every completed
- * call leaves it ready for the next, whatever that call's batch size.  Calls
- * that share a workspace must not overlap (issue them on one stream).
+ * workspace must be zero-filled once before its first use (a workspace that
+ * was not is not detected); every call leaves it ready for the next,
+ * whatever that call's batch size.  Calls that share a workspace must not
+ * overlap (issue them on one stream).
  */
 int64_t akv_compact_workspace_bytes(int32_t n_requests, int64_t total_tokens);
 
 /*
- * Kernel launches akv_compact_rows makes on the current device for a batch
- * of n_requests holding total_tokens raw tokens whose largest list (fresh
- * slots, retired / kept / kv_indices capacity) holds largest_list entries:
- * 1 (one launch, every tile resident at once) or 2; 0 for an empty batch,
- * AKV_EINVAL for negative sizes.  When tile_tokens is not NULL it receives
- * the tokens per tile of that path (0 for an empty batch).  No device work.
- * No counterpart in the reference: it tells a caller which path (and which
- * status bits) to expect.
+ * Passes akv_compact_rows makes over the tokens on the current device for a
+ * batch of n_requests holding total_tokens raw tokens whose largest list
+ * (fresh slots, retired / kept / kv_indices capacity) holds largest_list
+ * entries: 1 (one kernel over every tile, the tiles meeting at an in-kernel
+ * barrier, then a one-workgroup finishing launch) or 2 (a count launch,
+ * then a scatter launch); 0 for an empty batch, AKV_EINVAL for negative
+ * sizes.  Either way the call makes two launches.  When tile_tokens is not
+ * NULL it receives the tokens per tile of that path (0 for an empty batch).
+ * No device work.  No counterpart in the reference: it tells a caller which
+ * path to expect.
  */
 int akv_compact_launches(int32_t n_requests, int64_t total_tokens,
                          int64_t largest_list, int64_t* tile_tokens);
@@ -112,22 +161,25 @@ int akv_compact_launches(int32_t n_requests, int64_t total_tokens,
  *   kv_indptr  (opt.)   [B+1] exclusive scan of kept + generated
  *   last_page_len (opt.) [B] ((kept + generated - 1) % page_size) + 1, 0 if empty
  *   counts     (opt.)   [B,3] kept, moved, retired
- *   status     (opt.)   device int32: 0, or bit 0 if fresh_count or a
- *                       capacity does not match; bit 1 if the one-launch
- *                       path's barrier did not complete and bit 2 if a tile
- *                       stopped waiting at it (a workspace that was not
- *                       zero-filled, or a device shared so heavily that the
- *                       tiles could not all run at once).  Outputs are
- *                       partial unless it reads 0.
+ *   status     (opt.)   device int32, AKV_STATUS_* bits: 0 when the
+ *                       outputs are complete; AKV_STATUS_SIZES when
+ *                       fresh_count or a capacity does not match the batch;
+ *                       AKV_STATUS_REBUILT when the one-pass path's
+ *                       finishing launch rebuilt the outputs of tiles that
+ *                       stopped waiting at its barrier.  Never read on the
+ *                       host here: pass it to the consumers' status
+ *                       argument, which then skip their work on the device
+ *                       when the outputs are unusable.
  * retired, the copy lists and raw_indices / active_positions may be NULL
  * when retired_capacity, fresh_count and kept_capacity are 0.
- * One launch when the batch has at most 512 requests, fewer than 2^29
- * tokens (and list capacities) and some tile size lets every tile run on
- * the device at once
- * (tiles publish counts; groups of 64 tiles are released in order, each
- * by its last arrival after summing the earlier groups' totals);
- * otherwise two launches: per-tile counts, then per-tile prefixes and every
- * output.
+ * One pass when the batch has at most 512 requests, fewer than 2^29
+ * tokens (and list capacities) and some tile size lets every tile be
+ * resident at once: tiles publish tagged counts, groups of 64 tiles are
+ * released in order, each by its last arrival after summing the earlier
+ * groups' totals, and a one-workgroup finishing launch rebuilds the
+ * outputs of any tile whose bounded wait ran out (so the outputs never
+ * depend on every tile actually being resident); otherwise two passes:
+ * per-tile counts, then per-tile prefixes and every output.
  * Replaces the CPU numpy/H2D path of OccurrenceState.advance +
  * terminal_slots + ReqToTokenPool.write + ContextDecodeLayout.from_layout,
  * akv/system/sglang/srt/context_system/occurrence.py:47-66,632-767 and
@@ -193,6 +245,9 @@ int akv_compact_pages(int32_t n_requests, const int64_t* req_offsets,
  *   active else prompt + start + i - active (raw = start + i when raw_ids_ptr
  *   is 0); T(x) = mapping[x] * multiplier when mapping != NULL.
  * rows/lengths/indptr/output/starts/mapping take AKV_I32 or AKV_I64.
+ * status (opt.): the akv_compact_rows status word when the registry's raw
+ * ids or the rows come from that call; nothing is read through them or
+ * written when (*status & AKV_STATUS_UNUSABLE) != 0.
  * Replaces context_decode_indices,
  * akv/system/sglang/kernels/ops/attention/context_page_table.py:34-76.
  */
@@ -203,7 +258,7 @@ int akv_decode_indices(const int64_t* registry, const int32_t* table,
                        int32_t output_dtype, const void* starts,
                        int32_t starts_dtype, const void* mapping,
                        int32_t mapping_dtype, int64_t multiplier,
-                       int32_t n_requests, void* stream);
+                       int32_t n_requests, const int32_t* status, void* stream);
 
 /*
  * Sliding-window visible key counts (inclusive q_pos - k_pos <= window),
@@ -277,6 +332,9 @@ int64_t akv_decode_attention_workspace_bytes(int32_t n_requests,
  *   kv_indptr[b+1]) (no sink term when sinks == NULL).  bf16 q / K / V,
  * head_dim 64 or 128, at most 16 q heads per KV head; max_len bounds every
  * request's key count (it sizes the split).  out is bf16 or f32.
+ * status (opt.): the akv_compact_rows status word when kv_indptr /
+ * kv_indices come from that call; no key index is read and nothing is
+ * written when (*status & AKV_STATUS_UNUSABLE) != 0.
  * The consumer of the compacted metadata (the reference's sink
  * normalisation o * sigmoid(lse - sink),
  * akv/system/sglang/srt/layers/attention/context_backend.py:254-272, over the
@@ -292,7 +350,8 @@ int akv_decode_attention(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                          float scale, void* out, int32_t out_dtype,
                          int64_t out_stride_b, int64_t out_stride_h,
                          int64_t max_len, void* workspace,
-                         int64_t workspace_bytes, void* stream);
+                         int64_t workspace_bytes, const int32_t* status,
+                         void* stream);
 
 /*
  * akv_decode_attention without a workspace argument, for callers that cannot
@@ -316,7 +375,8 @@ int akv_decode_attention_noalloc(const void* q, int64_t q_stride_b,
                                  const int32_t* kv_indices, const float* sinks,
                                  float scale, void* out, int32_t out_dtype,
                                  int64_t out_stride_b, int64_t out_stride_h,
-                                 int64_t max_len, void* stream);
+                                 int64_t max_len, const int32_t* status,
+                                 void* stream);
 
 /*
  * Prefill context attention over occurrence metadata (MFMA, bf16 in, fp32
@@ -476,10 +536,13 @@ int akv_bind_occurrences(int32_t n_requests, const int64_t* bases,
  * (dst_v_ptrs[l]); a NULL slot vector means slot t (a packed buffer).
  * Pointer tables are DEVICE arrays of n_layers base addresses; strides are
  * bytes between slots; rows, strides and bases are 16-byte aligned.
- * Destinations may be peer-GPU addresses.  Replaces the compacted
- * final-version transfer's gather/scatter of request_active_slots and the
- * D-side destination fill, akv/system/sglang/srt/disaggregation/
- * context_transfer.py:110-128,201-259 (the transport itself is external).
+ * Destinations may be peer-GPU addresses.  status (opt.): the
+ * akv_compact_rows status word when a slot vector comes from that call; no
+ * row is read or written when (*status & AKV_STATUS_UNUSABLE) != 0.
+ * Replaces the compacted final-version transfer's gather/scatter of
+ * request_active_slots and the D-side destination fill,
+ * akv/system/sglang/srt/disaggregation/context_transfer.py:110-128,201-259
+ * (the transport itself is external).
  */
 int akv_copy_kv_rows(const uint64_t* src_k_ptrs, const uint64_t* src_v_ptrs,
                      const uint64_t* dst_k_ptrs, const uint64_t* dst_v_ptrs,
@@ -487,7 +550,7 @@ int akv_copy_kv_rows(const uint64_t* src_k_ptrs, const uint64_t* src_v_ptrs,
                      int64_t src_k_stride, int64_t src_v_stride,
                      int64_t dst_k_stride, int64_t dst_v_stride,
                      const int32_t* src_slots, const int32_t* dst_slots,
-                     int64_t n_tokens, void* stream);
+                     int64_t n_tokens, const int32_t* status, void* stream);
 
 /*
  * Host event compiler (CPU, no device work).  Replays Drop and Reposition

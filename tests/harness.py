@@ -61,7 +61,8 @@ class DecodeRows:
         return cls(torch.from_numpy(table).to(device), dev, host)
 
 
-def window_indices(rows, table, row_ids, seq_lens, window, indptr, output, *, mapping=None, multiplier=1):
+def window_indices(rows, table, row_ids, seq_lens, window, indptr, output, *, mapping=None, multiplier=1,
+                   status=None):
     """Sliding-window read indices: visible counts, their offsets, the slots."""
     lengths = torch.empty_like(seq_lens)
     starts = torch.empty_like(seq_lens)
@@ -69,7 +70,7 @@ def window_indices(rows, table, row_ids, seq_lens, window, indptr, output, *, ma
     indptr = indptr[: len(seq_lens) + 1]
     page_table.build_indptr(lengths, indptr)
     page_table.context_decode_indices(rows, table, row_ids, lengths, indptr, output, starts=starts,
-                                      mapping=mapping, multiplier=multiplier)
+                                      mapping=mapping, multiplier=multiplier, status=status)
     return indptr, lengths, starts
 
 

@@ -339,17 +339,42 @@ def torch_layout(layout):
 
 class NativeImpl:
     """``akv_amd.ownership`` (C++ host planner + device gathers) behind the
-    scenario interface; slots live on ``device`` as ``slot_dtype``."""
+    scenario interface; slots live on ``device`` as ``slot_dtype``.
+
+    The window, the plan, the advance (bind) and the terminal slots run
+    natively.  The radix-cache bookkeeping around them -- matches, borrowed
+    gaps, the choice of published terminal versions, publication, Drop of
+    borrowed owners, private-page and SWA queries -- is the reference
+    scheduler's and is not part of the product; here it is played by the
+    oracle's ``State`` (pinned by the same golden traces) on host copies of
+    the native state's fields."""
 
     def __init__(self, device, slot_dtype=None):
         import torch
 
         from akv_amd import occurrence, ownership
+        from oracle import ownership as oracle_ownership
 
         self.torch, self.occ, self.own = torch, occurrence, ownership
+        self.oracle = oracle_ownership
         self.device = device
         self.dtype = slot_dtype or torch.int64
         self._layouts = {}
+
+    def _to_oracle(self, st):
+        n = self._n
+        return self.oracle.State(n(st.slots).astype(np.int64), n(st.owned).copy(), n(st.canonical_rows).copy(),
+                                 n(st.terminal_rows).copy(), n(st.canonical_positions).copy(),
+                                 int(st.exact_prefix_len), None if st.swa_resident is None else n(st.swa_resident).copy())
+
+    def _from_oracle(self, ost):
+        t = self.torch
+        return self.own.OccurrenceState(
+            self._slots(ost.slots), t.from_numpy(np.asarray(ost.owned, dtype=bool).copy()),
+            t.from_numpy(np.asarray(ost.canonical_rows, dtype=np.int64).copy()),
+            t.from_numpy(np.asarray(ost.terminal_rows, dtype=np.int64).copy()),
+            t.from_numpy(np.asarray(ost.canonical_positions, dtype=np.int32).copy()), int(ost.exact_prefix_len),
+            None if ost.swa_resident is None else t.from_numpy(np.asarray(ost.swa_resident, dtype=bool).copy()))
 
     def _t(self, a, dtype=None, device=None):
         t = self.torch.from_numpy(np.ascontiguousarray(a).copy())
@@ -380,16 +405,15 @@ class NativeImpl:
                     ends=w.segment_query_ends.numpy(), key_offsets=w.segment_key_offsets.numpy(), _obj=w)
 
     def from_match(self, slots, positions, exact, resident, swa):
-        return self.own.OccurrenceState.from_match(
-            self._slots(slots), self._t(positions, self.torch.int32), exact_prefix_len=int(exact),
-            resident=self._bool(resident), swa_resident=self._bool(swa))
+        return self._from_oracle(self.oracle.State.from_match(slots, positions, exact_prefix_len=exact,
+                                                              resident=resident, swa_resident=swa))
 
     def gap(self, st, slots, positions, resident, end, exact, swa):
-        return st.reuse_match_gap(self._slots(slots), self._t(positions, self.torch.int32), self._bool(resident),
-                                  int(end), exact_prefix_len=int(exact), swa_resident=self._bool(swa))
+        return self._from_oracle(self._to_oracle(st).reuse_match_gap(
+            slots, positions, resident, end, exact_prefix_len=exact, swa_resident=swa))
 
     def keep(self, st, layout, qe):
-        return st.prefill_terminal_keep(self._layout(layout), int(qe)).numpy()
+        return self._to_oracle(st).prefill_terminal_keep(layout, qe)
 
     @staticmethod
     def _plan_dict(p):
@@ -426,19 +450,19 @@ class NativeImpl:
         return self._n(st.terminal_slots())
 
     def terminal_swa(self, st):
-        return self._n(st.terminal_swa_residency())
+        return self._to_oracle(st).terminal_swa_residency()
 
     def publish(self, st, matched, cache_len, swa):
-        return st.publish(self._slots(matched), cache_len=cache_len, swa_resident=self._bool(swa))
+        return self._from_oracle(self._to_oracle(st).publish(matched, cache_len=cache_len, swa_resident=swa))
 
     def drop(self, st, mask):
-        return st.drop_borrowed_raw(self._bool(mask))
+        return self._from_oracle(self._to_oracle(st).drop_borrowed_raw(mask))
 
     def private(self, st):
-        return self._n(st.private_slots())
+        return self._to_oracle(st).private_slots()
 
     def nonterminal(self, st):
-        return self._n(st.nonterminal_private_slots())
+        return self._to_oracle(st).nonterminal_private_slots()
 
     def nonterminal_residency(self, st):
-        return self._n(st.nonterminal_private_residency())
+        return self._to_oracle(st).nonterminal_private_residency()

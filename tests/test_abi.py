@@ -185,12 +185,3 @@ def test_native_compiler_error_messages(kw, message):
     ev.update(kw)
     with pytest.raises(ValueError, match=re.escape(message)):
         plan.compile_context_layout(**ev)
-
-
-def test_append_generated_layout():
-    ev = _events(10, [(10, [(2, 4)])], [9])
-    lay = plan.compile_context_layout(**ev)
-    ext = plan.append_generated_layout(lay, [5, 6, 7])
-    assert ext.next_position == lay.next_position + 3
-    assert ext.positions[-3:].tolist() == [8, 9, 10]
-    assert ext.keep_mask[-3:].all()

@@ -118,11 +118,11 @@ def test_gpt_oss_decode_after_drop_and_reposition(device):
     rows = torch.arange(B, dtype=torch.int64, device=device)
     tables.compact_rows(inputs, table, rows, fresh, out, generated=torch.ones(B, dtype=torch.int32, device=device),
                         birth_slots=birth)
-    tables.check_status(out)  # the lists feed the Reposition below
     pool = synth.make_pool(model, w.pool_slots, device, seed=9, generate_on_device=True)
     rope = synth.rope_table(w, device)
-    ops.reposition_kv_layers(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], out.copy_src, out.copy_dst,
-                             out.copy_pairs, rope)
+    # the lists feed the Reposition on the device, gated by the status word
+    ops.reposition_kv_layers_gated(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], out.copy_src, out.copy_dst,
+                                   out.copy_pairs, rope, status=out.status)
 
     # registry rows straight from the compaction outputs
     kept_off = np.concatenate(([0], np.cumsum(inputs.kept)))
@@ -133,7 +133,7 @@ def test_gpt_oss_decode_after_drop_and_reposition(device):
     window = 128
     win_indptr = torch.zeros(B + 1, dtype=torch.int32, device=device)
     win_idx = torch.zeros(B * (window + 1), dtype=torch.int32, device=device)
-    window_indices(registry, table, rows, seq, window, win_indptr, win_idx)
+    window_indices(registry, table, rows, seq, window, win_indptr, win_idx, status=out.status)
 
     g = torch.Generator().manual_seed(5)
     q = torch.randn((B, 64, 64), generator=g).to(torch.bfloat16).to(device)
@@ -143,9 +143,10 @@ def test_gpt_oss_decode_after_drop_and_reposition(device):
                                           (out.kv_indptr, out.kv_indices, max(inputs.kept) + 1))):
         o = torch.empty((B, 64, 64), dtype=torch.bfloat16, device=device)
         attention.decode_attention(q, pool.k[layer], pool.v[layer], ip, ix, o, scale=0.125, max_len=mx,
-                                   sinks=sinks[layer])
+                                   sinks=sinks[layer], status=out.status)
         outs.append(o)
     torch.cuda.synchronize()
+    assert tables.check_status(out) == 0
 
     win_ip, win_ix = win_indptr.cpu().numpy(), win_idx.cpu().numpy()
     full_ip, full_ix = out.kv_indptr.cpu().numpy(), out.kv_indices.cpu().numpy()

@@ -182,7 +182,6 @@ def test_pipeline_compaction_feeds_registry(device):
     gen = torch.ones(w.n_requests, dtype=torch.int32, device=device)
     row_ids = torch.arange(w.n_requests, dtype=torch.int64, device=device)
     tables.compact_rows(inputs, table, row_ids, fresh, out, generated=gen)
-    tables.check_status(out)  # the decode layout feeds the index kernels below
     kept_off = np.concatenate(([0], np.cumsum(inputs.kept)))
     rows = []
     for b, lay in enumerate(layouts):
@@ -194,8 +193,11 @@ def test_pipeline_compaction_feeds_registry(device):
     indptr = torch.empty(w.n_requests + 1, dtype=torch.int32, device=device)
     pt.build_indptr(seq, indptr)
     kv = torch.empty(int(seq.sum()), dtype=torch.int32, device=device)
-    pt.context_decode_indices(registry, table, row_ids, seq, indptr, kv)
+    # the decode layout feeds the index kernel on the device, gated by the
+    # compaction's status word
+    pt.context_decode_indices(registry, table, row_ids, seq, indptr, kv, status=out.status)
     torch.cuda.synchronize()
+    assert tables.check_status(out) == 0
     assert torch.equal(kv, out.kv_indices)
     assert torch.equal(indptr, out.kv_indptr)
 

@@ -41,14 +41,12 @@ def test_graph_replays_match_eager(device):
 
     def step():
         tables.compact_rows(inputs, table, rows, fresh, out, generated=gen, birth_slots=birth)
-        ops.reposition_kv_layers(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], out.copy_src, out.copy_dst,
-                                 out.copy_pairs, rope)
+        ops.reposition_kv_layers_gated(pool.k_ptrs, pool.v_ptrs, pool.k[0], pool.v[0], out.copy_src,
+                                       out.copy_dst, out.copy_pairs, rope, status=out.status)
         page_table.build_indptr(seq, indptr)
-        page_table.context_decode_indices(registry, table, rows, seq, indptr, kv)
+        page_table.context_decode_indices(registry, table, rows, seq, indptr, kv, status=out.status)
 
     dst = fresh.long()
-    tables.compact_rows(inputs, table, rows, fresh, out, generated=gen, birth_slots=birth)
-    tables.check_status(out)  # before any list reaches the Reposition
     step()
     torch.cuda.synchronize()
     want = [t.clone() for t in (table, out.retired, out.copy_src, out.copy_pairs, out.kv_indices, kv, indptr)]
@@ -77,6 +75,7 @@ def test_graph_replays_match_eager(device):
         got = [table, out.retired, out.copy_src, out.copy_pairs, out.kv_indices, kv, indptr]
         for g, x in zip(got, want):
             assert torch.equal(g, x), f"replay {replay}"
+        assert int(out.status.item()) == 0, f"replay {replay}"
         for t, x in zip(pool.k + pool.v, want_kv):
             assert torch.equal(t[dst].view(torch.int16), x.view(torch.int16)), f"replay {replay}"
     assert np.array_equal(kv.cpu().numpy(), out.kv_indices.cpu().numpy())

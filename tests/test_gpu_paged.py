@@ -123,6 +123,63 @@ def test_shared_prefix_cow_bit_exact(device, name, groups):
         assert storage_equal(to_storage(pool.k[l][s_dst]), kk[0][m:]), f"layer {l}"
 
 
+def test_cow_one_group_all_32_layers(device):
+    """The full Llama-3-8B copy-on-write workload's first request group (4
+    requests over the shared 8192-token prefix, 394,728 tokens) at all 32
+    layers (a 92 GiB pool): tables bit-exact, V moved bit for bit and every
+    other slot unchanged (per-layer checksums) in full, K against the
+    torch-CPU restatement on a seeded sample of 6000 copies per layer (every
+    same-position copy included)."""
+    from oracle import cpu_torch
+
+    full = synth.workload("llama3-cow-16")
+    w = dataclasses.replace(full, lengths=full.lengths[:4], spans=full.spans[:4])
+    assert w.model.n_layers == 32
+    B = w.n_requests
+    a = synth.assign_pages(w)
+    layouts = synth.compile_layouts(w)
+    P = w.page_size
+    slots = a.pool_pages * P
+    print(f"cow one group: {B} requests, {sum(w.lengths)} tokens, {a.pool_pages} pages, 32 layers", flush=True)
+    pool = synth.make_pool(w.model, slots, device, seed=4, generate_on_device=True)
+    cos_sin = synth.rope_table(w, device)
+    order = np.arange(B)
+    table = _table_for(a.birth_rows, max(w.lengths) + 5, device, order)
+    # the copies' destinations are fresh pages: every other slot keeps its bits
+    fresh = np.concatenate(a.fresh_pages).astype(np.int64)
+    touched = torch.zeros(slots, dtype=torch.bool, device=device)
+    if len(fresh):
+        fresh_d = torch.from_numpy(fresh).to(device)
+        touched.view(-1, P)[fresh_d] = True
+    keep_sum = [t[~touched].view(torch.int16).to(torch.int64).sum().item() for t in pool.k + pool.v]
+    got = _run_groups(w, a, layouts, table, order, device, pool, cos_sin)
+    torch.cuda.synchronize()
+    _check_tables(w, a, layouts, got, table, order)
+    after_sum = [t[~touched].view(torch.int16).to(torch.int64).sum().item() for t in pool.k + pool.v]
+    assert after_sum == keep_sum
+    src = np.concatenate([got[b]["copy_source_slots"] for b in range(B)]).astype(np.int64)
+    dst = np.concatenate([got[b]["copy_destination_slots"] for b in range(B)]).astype(np.int64)
+    pairs = np.concatenate([got[b]["copy_position_pairs"] for b in range(B)])
+    assert len(np.unique(dst)) == len(dst) and not np.isin(dst, src).any()
+    src_d = torch.from_numpy(src).to(device)
+    dst_d = torch.from_numpy(dst).to(device)
+    rng = np.random.default_rng(2)
+    same = np.flatnonzero(pairs[:, 0] == pairs[:, 1])
+    sample = np.union1d(rng.choice(len(src), size=min(len(src), 6000), replace=False), same)
+    m = len(sample)
+    s_idx = torch.from_numpy(sample).to(device)
+    # source rows are never overwritten (fresh destinations), so they still
+    # hold the pre-Reposition values
+    host_k = [torch.cat((t[src_d[s_idx]].cpu(), torch.zeros_like(t[src_d[s_idx]].cpu()))) for t in pool.k]
+    host_v = [torch.zeros_like(h) for h in host_k]
+    cpu_torch.reposition_kv_layers(host_k, host_v, np.arange(m), np.arange(m, 2 * m), pairs[sample], cos_sin.cpu(),
+                                   is_neox_style=w.model.is_neox_style)
+    for l in range(w.model.n_layers):
+        assert torch.equal(pool.v[l][dst_d].view(torch.int16), pool.v[l][src_d].view(torch.int16)), f"V layer {l}"
+        got_k = pool.k[l][dst_d[s_idx]].cpu()
+        assert torch.equal(got_k.view(torch.int16), host_k[l][m:].view(torch.int16)), f"K layer {l}"
+
+
 def _edge_workload():
     # raggeds tails, a drop at token 0 (every page copied), a drop on a page
     # boundary, one inside the last page, and a request with no drop at all

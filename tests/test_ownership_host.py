@@ -87,36 +87,31 @@ def test_reference_messages(cpu_gather):
     with pytest.raises(ValueError, match="does not cover the planned queries"):
         ownership.plan_occurrence_materialization(win, pos, z, z, z, keep[:-1], query_start=2, query_end=n - 1,
                                                   exact_prefix_len=0)
-    with pytest.raises(ValueError, match="Invalid Context match ownership metadata"):
-        ownership.OccurrenceState.from_match(torch.zeros(3, dtype=torch.int64), torch.zeros(2, dtype=torch.int32),
-                                             exact_prefix_len=0)
-    st = ownership.OccurrenceState.from_match(torch.arange(2), lay.positions[:2].clone(), exact_prefix_len=2)
-    p = st.plan(win, st.prefill_terminal_keep(lay, n))
+    st = impl.from_match(np.arange(2), sc["layout"].positions[:2], 2, np.ones(2, dtype=bool), None)
+    p = st.plan(win, torch.from_numpy(impl.keep(st, sc["layout"], n)))
     with pytest.raises(ValueError, match="Context admission does not cover the selected window"):
         st.advance(win, p, torch.arange(n - 3), torch.arange(p.extra_page_count), torch.from_numpy(sc["visible"]))
-    with pytest.raises(ValueError, match="Distinct raw tokens|must cover the raw terminal table"):
-        st.publish(torch.zeros(5, dtype=torch.int64))
-    with pytest.raises(ValueError, match="Drop ownership mask"):
-        st.drop_borrowed_raw(torch.zeros(7, dtype=torch.bool))
+    with pytest.raises(ValueError, match="Occurrence slots must be int32 or int64"):
+        ownership.OccurrenceState.empty(torch.device("cpu"), torch.int16)
 
 
-def test_free_context_slots_splits_by_swa_residency(cpu_gather):
-    class Alloc:
-        def __init__(self):
-            self.calls = []
-
-        def free(self, s):
-            self.calls.append(("free", s.tolist()))
-
-        def free_full(self, s):
-            self.calls.append(("free_full", s.tolist()))
-
-    a = Alloc()
-    slots = torch.tensor([5, 6, 7, 8])
-    ownership.free_context_slots(a, slots, torch.tensor([True, False, True, False]))
-    ownership.free_context_slots(a, slots, None)
-    ownership.free_context_slots(a, slots, torch.zeros(4, dtype=torch.bool))
-    assert a.calls == [("free", [5, 7]), ("free_full", [6, 8]), ("free", [5, 6, 7, 8]), ("free_full", [5, 6, 7, 8])]
+def test_empty_state_plans_like_an_unmatched_request(cpu_gather):
+    """OccurrenceState.empty equals the state of a request whose match is
+    empty, field for field, and plans the same first forward."""
+    impl = scenarios.NativeImpl(torch.device("cpu"))
+    sc = scenarios.make(7)
+    n = sc["n"]
+    empty = ownership.OccurrenceState.empty(torch.device("cpu"))
+    matched = impl.from_match(np.zeros(0, np.int64), np.zeros(0, np.int32), 0, np.zeros(0, dtype=bool), None)
+    for name in ("slots", "owned", "canonical_rows", "terminal_rows", "canonical_positions"):
+        a, b = getattr(empty, name), getattr(matched, name)
+        assert a.dtype == b.dtype and a.shape == b.shape, name
+    assert empty.exact_prefix_len == 0 and empty.swa_resident is None
+    win = impl.window(sc["layout"], sc["visible"], 0, n)
+    keep = impl.keep(empty, sc["layout"], n)
+    pa, pb = impl.plan(empty, win, keep), impl.plan(matched, win, keep)
+    for key in ("source_rows", "allocated", "copy_source_rows", "pairs", "terminal_occurrences"):
+        assert np.array_equal(pa[key], pb[key]), key
 
 
 def test_long_lifecycles_match_the_oracle(cpu_gather):
@@ -134,3 +129,34 @@ def test_long_lifecycles_match_the_oracle(cpu_gather):
             assert _same(a, b), (seed, name)
         forwards += sum(1 for k, _ in want if k.endswith(".keep"))
     assert forwards > 60
+
+
+def test_bench_published_terminals_match_the_scheduler_rule(cpu_gather):
+    """The benchmark's chunked lifecycle picks each forward's published
+    terminal versions with its own helper; it equals the rule of the
+    reference scheduler (played by the oracle) at every forward of random
+    multi-forward scenarios."""
+    import bench
+
+    impl = scenarios.NativeImpl(torch.device("cpu"))
+    checked = 0
+    for seed in range(12):
+        sc = scenarios.make(300 + seed)
+        n = sc["n"]
+        st = impl.from_match(np.zeros(0, np.int64), np.zeros(0, np.int32), 0, np.zeros(0, dtype=bool), None)
+        bounds = sorted({0, n, *[int(b) for b in sc["forwards"] if 0 < b < n]})
+        lay = scenarios.torch_layout(sc["layout"])
+        for qs, qe in zip(bounds[:-1], bounds[1:]):
+            want = impl.keep(st, sc["layout"], qe)
+            got = bench._published_terminals(st, lay, qe).numpy()
+            assert np.array_equal(got, want), (seed, qs, qe)
+            checked += 1
+            win = impl.window(sc["layout"], sc["visible"], qs, qe)
+            try:
+                p = impl.plan(st, win, want)
+            except ValueError:
+                break
+            q = impl._slots(10_000 * (qs + 1) + np.arange(qe - qs))
+            extra = impl._slots(900_000 + 10_000 * qs + np.arange(p["extra_page_count"]))
+            st, _ = impl.advance(st, win, p, q, extra, sc["visible"])
+    assert checked > 20

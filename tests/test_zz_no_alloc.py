@@ -41,7 +41,7 @@ def _noalloc(c, out, scale):
         q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0),
         v.stride(1), n, hq, k.shape[1], d, c["indptr"].data_ptr(), c["indices"].data_ptr(), c["sinks"].data_ptr(),
         scale, out.data_ptr(), _lib.AKV_F32 if out.dtype == torch.float32 else _lib.AKV_BF16, out.stride(0),
-        out.stride(1), c["max_len"], current_stream_handle(q.device))
+        out.stride(1), c["max_len"], None, current_stream_handle(q.device))
     _lib.check(rc, "akv_decode_attention_noalloc")
 
 
