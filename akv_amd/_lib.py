@@ -86,7 +86,7 @@ _SIGNATURES = {
         c_int32,
         [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64,
          c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, _P, _P, c_int32, _P, c_int32, _P, _P,
-         c_int32, c_int32, _P, ctypes.c_float, _P, c_int32, c_int64, c_int64, c_int64, _P],
+         c_int32, c_int32, _P, ctypes.c_float, ctypes.c_float, _P, c_int32, c_int64, c_int64, c_int64, _P],
     ),
     "akv_bind_workspace_bytes": (c_int64, [c_int32, c_int64]),
     "akv_bind_occurrences": (

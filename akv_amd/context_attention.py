@@ -33,12 +33,13 @@ def extend_attention_fwd(q_extend, k_extend, v_extend, o_extend, k_buffer, v_buf
     ``k_extend``/``v_extend`` ``[Nq, Hkv, D]`` (this forward's K/V),
     ``k_buffer``/``v_buffer`` the layer's pool ``[slots, Hkv, D]``; prefix rows
     ``kv_indices[kv_indptr[s]:kv_indptr[s+1]]``; queries causal over their own
-    keys.  Supported: bf16 inputs, bf16 or f32 output, head_dim 64 or 128,
-    a GQA group (q heads per KV head) that divides 128 (1, 2, 4, ..., 128;
-    e.g. 28 q heads over 4 KV heads is rejected), row strides that are
-    multiples of 8 elements, causal, no custom mask, no logit cap, unit K/V
-    scales; anything else raises ``ValueError``.  The reference's Triton
-    kernel accepts any group and head dim; these are this kernel's limits.
+    keys.  Supported: bf16 inputs, bf16 or f32 output, head dims that are
+    multiples of 8 up to 128, any GQA group of up to 128 q heads per KV
+    head, logit caps (``cap * tanh(score / cap)``), row strides that are
+    multiples of 8 elements, causal, no custom mask, unit K/V scales;
+    anything else raises ``ValueError`` (the reference's Triton kernel also
+    takes wider heads, Q/K and V heads of different widths, custom masks and
+    KV scales).
     """
     use_context_positions = context_q_positions is not None
     if use_context_positions != (context_kv_positions is not None):
@@ -55,8 +56,10 @@ def extend_attention_fwd(q_extend, k_extend, v_extend, o_extend, k_buffer, v_buf
             raise ValueError("Context attention positions must share one dtype")
     if custom_mask is not None or mask_indptr is not None or not is_causal:
         raise ValueError("only causal extend attention without a custom mask is supported")
-    if logit_cap or k_scale != 1.0 or v_scale != 1.0 or window_kv_offsets is not None or xai_temperature_len > 0:
-        raise ValueError("logit caps, KV scales, window KV offsets and temperature scaling are not supported")
+    if k_scale != 1.0 or v_scale != 1.0 or window_kv_offsets is not None or xai_temperature_len > 0:
+        raise ValueError("KV scales, window KV offsets and temperature scaling are not supported")
+    if logit_cap is None or not logit_cap >= 0.0 or logit_cap == float("inf"):
+        raise ValueError("logit_cap must be 0 (no cap) or positive and finite")
     for t in (q_extend, k_extend, v_extend, k_buffer, v_buffer):
         if t.dtype != torch.bfloat16 or t.ndim != 3 or t.stride(-1) != 1:
             raise ValueError("q/k/v and the KV pool must be bf16 [tokens, heads, head_dim] with unit dim stride")
@@ -91,7 +94,7 @@ def extend_attention_fwd(q_extend, k_extend, v_extend, o_extend, k_buffer, v_buf
             kv_indices.data_ptr() if kv_indices.numel() else None, _INDEX[kv_indices.dtype],
             _lib.ptr(context_q_positions), _lib.ptr(context_kv_positions), pos_dtype,
             int(sliding_window_size) if sliding_window_size is not None else -1,
-            _lib.ptr(sinks), float(scale), o_extend.data_ptr(),
+            _lib.ptr(sinks), float(scale), float(logit_cap), o_extend.data_ptr(),
             _lib.AKV_F32 if o_extend.dtype == torch.float32 else _lib.AKV_BF16,
             o_extend.stride(0), o_extend.stride(1), int(max_len_extend),
             current_stream_handle(q_extend.device),

@@ -95,6 +95,8 @@ struct CtxArgs {
   float scale_log2;
   int32_t out_f32;
   int32_t group, group_shift, tokens_per_block, kv_heads;
+  int32_t head_dim;   // head dims in use (<= the kernel's D; the rest are zero)
+  float cap, cap_log2;  // logit cap (scores -> cap tanh(score / cap)), cap log2(e)
 };
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -172,7 +174,10 @@ __device__ __forceinline__ int32_t rel_pos(int64_t p, int64_t base) {
 // KEYS keys per tile: 128 for full layers at head_dim 64 (half the tile
 // barriers, staging and commits per key), 64 for windowed layers (less of a
 // tile outside the window) and at head_dim 128 (LDS for two workgroups per CU)
-template <int D, int KEYS, typename IdxT, typename PosT, bool POS>
+// GEN: the general instance -- logit caps, heads narrower than D (the dims
+// past head_dim zero in the tiles), groups padded to a power of two; the
+// plain instance takes none of these checks.
+template <int D, int KEYS, typename IdxT, typename PosT, bool POS, bool GEN>
 __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const CtxArgs a) {
   constexpr int kSub = sub_tiles(D);
   constexpr int kKeys = KEYS;
@@ -190,8 +195,14 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   const bool i64 = a.indptr_i64;
   const int64_t qo0 = load_index(a.qo_indptr, i64, seg);
   const int32_t qlen = static_cast<int32_t>(load_index(a.qo_indptr, i64, seg + 1) - qo0);
-  const int G = a.group;
+  const int G = a.group;                         // q heads per KV head
+  const int gmask = (1 << a.group_shift) - 1;    // rows per token: G padded to a power of two
   const int T = a.tokens_per_block;
+  const int hd = GEN ? a.head_dim : D;
+  const bool cap = GEN && a.cap > 0.f;
+  // the score's log2-domain multiplier: with a cap the scores are capped
+  // (and scaled) before the softmax, which then takes them as they are
+  const float mult = cap ? 1.f : a.scale_log2;
   // KV head fastest: workgroup id mod 8 picks the XCD, so with 8 KV heads
   // every XCD streams one head's K/V through its own L2.  Token blocks run
   // last-first: the last blocks see the most causal keys, and starting them
@@ -264,13 +275,17 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   for (int s = 0; s < kSub; ++s) {
     const int r = row_of(s);
     const int tl = r >> a.group_shift;
-    const int head = g * G + (r & (G - 1));
-    const bool ok = t0 + tl < qlen;
-    if (quad == 0) rel_rows[r] = ok ? rel_pos(qpos_of(t0 + tl), qbase) : last_rel;
+    const int hl = r & gmask;
+    const int head = g * G + hl;
+    const bool tok = t0 + tl < qlen;
+    // a padding row (hl >= G) keeps Q = 0 and is never stored
+    const bool ok = tok && (!GEN || hl < G);
+    if (quad == 0) rel_rows[r] = tok ? rel_pos(qpos_of(t0 + tl), qbase) : last_rel;
 #pragma unroll
     for (int ks = 0; ks < kKSteps; ++ks) {
       u32x4 w = {0u, 0u, 0u, 0u};
-      if (ok)
+      // head dims past hd are zero
+      if (ok && (!GEN || 8 * (4 * ks + quad) < hd))
         w = load16(a.q + (qo0 + t0 + tl) * a.q_st + static_cast<int64_t>(head) * a.q_sh + 32 * ks + 8 * quad);
       qop[s][ks] = __builtin_bit_cast(bf16x8, w);
     }
@@ -320,8 +335,16 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
         krow = kpool_b + so * kp_sb;
         vrow = vpool_b + so * vp_sb;
       }
-      __builtin_amdgcn_global_load_lds(krow + 16 * ck, (lds_void*)(&t.k[blk * kRowsPerBlock][0]), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vrow + 16 * cv, (lds_void*)(&t.v[blk * kRowsPerBlock][0]), 16, 0, 0);
+      if (!GEN || hd == D) {
+        __builtin_amdgcn_global_load_lds(krow + 16 * ck, (lds_void*)(&t.k[blk * kRowsPerBlock][0]), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vrow + 16 * cv, (lds_void*)(&t.v[blk * kRowsPerBlock][0]), 16, 0, 0);
+      } else {
+        // narrower heads: chunks past hd are not loaded (they stay zero)
+        if (8 * ck < hd)
+          __builtin_amdgcn_global_load_lds(krow + 16 * ck, (lds_void*)(&t.k[blk * kRowsPerBlock][0]), 16, 0, 0);
+        if (8 * cv < hd)
+          __builtin_amdgcn_global_load_lds(vrow + 16 * cv, (lds_void*)(&t.v[blk * kRowsPerBlock][0]), 16, 0, 0);
+      }
     }
     // key positions matter only to a window (causal masking is by index)
     if (a.window >= 0 && tid < kKeys) {
@@ -367,6 +390,18 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   const bf16x8 kOnes = {__bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f),
                         __bf16(1.f), __bf16(1.f), __bf16(1.f), __bf16(1.f)};
 
+  if (GEN && hd < D) {
+    // narrower heads: the tiles' chunks past hd are never loaded; zero them
+    // once.  The stores cover every chunk, loaded ones too, so they must
+    // land before any wave's direct loads into tile 0: barrier first.
+    constexpr int kWords = KEYS * D / 8;  // 16 B chunks per array
+    for (int i = tid; i < 4 * kWords; i += kThreads) {
+      __bf16* arr = i < kWords ? &tile0.k[0][0] : i < 2 * kWords ? &tile0.v[0][0]
+                  : i < 3 * kWords ? &tile1.k[0][0] : &tile1.v[0][0];
+      reinterpret_cast<u32x4*>(arr)[i % kWords] = u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+  }
   if (n_pref > 0) fetch_slots(0);
   stage(0, tile0);
   if (1 < n_pref) fetch_slots(1);
@@ -417,6 +452,19 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
                                                                ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sh[j][s], 0, 0, 0);
         }
       }
+      if (cap) {
+        // capped logits: cap tanh(scale s / cap), in the log2 domain, before
+        // the mask (a masked score stays -inf); tanh(x) = 1 - 2 / (1 + e^2x)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int s = 0; s < kSub; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float e2x = __builtin_amdgcn_exp2f(sh[j][s][i] * a.scale_log2 * (2.f / a.cap));
+              sh[j][s][i] = a.cap_log2 * (1.f - 2.f * __builtin_amdgcn_rcpf(1.f + e2x));
+            }
+      }
       if (masked) {
 #pragma unroll
         for (int s = 0; s < kSub; ++s) {
@@ -446,7 +494,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
           float mx = max3(m0, m1, max3(sh[1][s][2], sh[1][s][3], -INFINITY));
           mx = row_max(mx);  // -inf when the row sees nothing here
           // the half's largest exponent, t - m in the log2 domain
-          const float top = fmaf(mx, a.scale_log2, neg_m[s]);
+          const float top = fmaf(mx, mult, neg_m[s]);
           const bool seen = lacc[s][0] != 0.f;
           const bool bump = seen ? top > kLazy : mx > -INFINITY;
           if (__builtin_amdgcn_ballot_w64(bump)) {
@@ -454,7 +502,7 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
             lacc[s] *= alpha;
 #pragma unroll
             for (int dt = 0; dt < kDTiles; ++dt) oacc[dt][s] *= alpha;
-            neg_m[s] = bump ? -(mx * a.scale_log2) : neg_m[s];
+            neg_m[s] = bump ? -(mx * mult) : neg_m[s];
           }
         }
       }
@@ -464,8 +512,8 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
         f32x4 e0, e1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          e0[i] = __builtin_amdgcn_exp2f(fmaf(sh[0][s][i], a.scale_log2, neg_m[s]));
-          e1[i] = __builtin_amdgcn_exp2f(fmaf(sh[1][s][i], a.scale_log2, neg_m[s]));
+          e0[i] = __builtin_amdgcn_exp2f(fmaf(sh[0][s][i], mult, neg_m[s]));
+          e1[i] = __builtin_amdgcn_exp2f(fmaf(sh[1][s][i], mult, neg_m[s]));
         }
         const bf16x4 b0 = __builtin_convertvector(e0, bf16x4);
         const bf16x4 b1 = __builtin_convertvector(e1, bf16x4);
@@ -566,20 +614,22 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   for (int s = 0; s < kSub; ++s) {
     float l = lacc[s][0];
     float scale = 1.f;
+    const int hl = row_of(s) & gmask;
     if (a.sinks) {
       const float m_run = l != 0.f ? -neg_m[s] : -INFINITY;
-      const float sink = a.sinks[g * G + (row_of(s) & (G - 1))] * kLog2e;
+      const float sink = a.sinks[g * G + (GEN && hl >= G ? G - 1 : hl)] * kLog2e;
       const float m_f = fmaxf(m_run, sink);
       scale = m_run == -INFINITY ? 0.f : exp2f(m_run - m_f);
       l = l * scale + exp2f(sink - m_f);
     }
     const float inv = l > 0.f ? scale / l : 0.f;
-    const int32_t row_token = row_of(s) >> a.group_shift, row_head = g * G + (row_of(s) & (G - 1));
-    if (t0 + row_token >= qlen) continue;
+    const int32_t row_token = row_of(s) >> a.group_shift, row_head = g * G + hl;
+    if (t0 + row_token >= qlen || (GEN && hl >= G)) continue;
     const int64_t at =
         (qo0 + t0 + row_token) * a.o_st + static_cast<int64_t>(row_head) * a.o_sh + 4 * quad;
 #pragma unroll
     for (int dt = 0; dt < kDTiles; ++dt) {
+      if (GEN && 16 * dt + 4 * quad >= hd) continue;
       const f32x4 o = oacc[dt][s] * inv;
       if (a.out_f32) {
         *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + at + 16 * dt) = o;
@@ -593,27 +643,37 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   }
 }
 
-template <int D, int KEYS, typename IdxT>
+template <int D, int KEYS, typename IdxT, bool GEN>
 void launch_pos(int pos, dim3 grid, hipStream_t st, const CtxArgs& a) {
   // pos: 0 none, 1 int32, 2 int64
   if (pos == 2)
-    hipLaunchKernelGGL((context_attention_kernel<D, KEYS, IdxT, int64_t, true>), grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((context_attention_kernel<D, KEYS, IdxT, int64_t, true, GEN>), grid, dim3(kThreads), 0, st, a);
   else if (pos == 1)
-    hipLaunchKernelGGL((context_attention_kernel<D, KEYS, IdxT, int32_t, true>), grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((context_attention_kernel<D, KEYS, IdxT, int32_t, true, GEN>), grid, dim3(kThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((context_attention_kernel<D, KEYS, IdxT, int64_t, false>), grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((context_attention_kernel<D, KEYS, IdxT, int64_t, false, GEN>), grid, dim3(kThreads), 0, st,
+                       a);
+}
+
+template <int D, int KEYS, typename IdxT>
+void launch_cap(int pos, dim3 grid, hipStream_t st, const CtxArgs& a) {
+  // the general instance for caps, narrower heads and padded groups
+  if (a.cap > 0.f || a.head_dim != D || a.group != (1 << a.group_shift))
+    launch_pos<D, KEYS, IdxT, true>(pos, grid, st, a);
+  else
+    launch_pos<D, KEYS, IdxT, false>(pos, grid, st, a);
 }
 
 template <int D, int KEYS>
 void launch_idx(bool idx64, int pos, dim3 grid, hipStream_t st, const CtxArgs& a) {
   if (idx64)
-    launch_pos<D, KEYS, int64_t>(pos, grid, st, a);
+    launch_cap<D, KEYS, int64_t>(pos, grid, st, a);
   else
-    launch_pos<D, KEYS, int32_t>(pos, grid, st, a);
+    launch_cap<D, KEYS, int32_t>(pos, grid, st, a);
 }
 
 void launch_typed(int head_dim, bool idx64, int pos, dim3 grid, hipStream_t st, const CtxArgs& a) {
-  if (head_dim == 128)
+  if (head_dim > 64)
     launch_idx<128, 64>(idx64, pos, grid, st, a);
   else if (a.window >= 0)
     launch_idx<64, 64>(idx64, pos, grid, st, a);
@@ -633,19 +693,24 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
                                      const void* kv_indptr, int32_t indptr_dtype, const void* kv_indices,
                                      int32_t indices_dtype, const void* q_positions, const void* kv_positions,
                                      int32_t positions_dtype, int32_t sliding_window, const float* sinks,
-                                     float scale, void* out, int32_t out_dtype, int64_t out_stride_t,
-                                     int64_t out_stride_h, int64_t max_query_len, void* stream) {
+                                     float scale, float logit_cap, void* out, int32_t out_dtype,
+                                     int64_t out_stride_t, int64_t out_stride_h, int64_t max_query_len,
+                                     void* stream) {
   using namespace akv;
   if (n_segments < 0 || max_query_len < 0) return fail(AKV_EINVAL, "akv_context_attention: negative size");
   if (n_segments == 0 || max_query_len == 0) return AKV_OK;
-  if (head_dim != 64 && head_dim != 128)
-    return fail(AKV_EINVAL, "akv_context_attention: head_dim %d (supported: 64, 128)", head_dim);
-  // the group of q heads per KV head divides every block's row count; a
-  // row packs its q head into 15 bits
-  if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0 || 128 % (q_heads / kv_heads) != 0 ||
-      q_heads > 32767)
-    return fail(AKV_EINVAL, "akv_context_attention: %d q heads over %d KV heads (group must divide 128)",
+  // heads of up to 128 dims in 16-byte chunks: the kernel's 64- or 128-dim
+  // tiles with the dims past head_dim zero
+  if (head_dim < 8 || head_dim > 128 || head_dim % 8 != 0)
+    return fail(AKV_EINVAL, "akv_context_attention: head_dim %d (supported: multiples of 8 up to 128)", head_dim);
+  // a block's rows are (token, q head) pairs with the group padded to a
+  // power of two (at most 128 q heads per KV head); a row packs its q head
+  // into 15 bits
+  if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0 || q_heads / kv_heads > 128 || q_heads > 32767)
+    return fail(AKV_EINVAL, "akv_context_attention: %d q heads over %d KV heads (at most 128 per KV head)",
                 q_heads, kv_heads);
+  if (!(logit_cap >= 0.f) || !std::isfinite(logit_cap))
+    return fail(AKV_EINVAL, "akv_context_attention: logit_cap must be 0 (none) or positive and finite");
   if (!valid_index_dtype(indptr_dtype) || !valid_index_dtype(indices_dtype) ||
       !valid_index_dtype(positions_dtype))
     return fail(AKV_EINVAL, "akv_context_attention: index vectors must be int32 or int64");
@@ -706,8 +771,12 @@ extern "C" int akv_context_attention(const void* q, int64_t q_stride_t, int64_t 
   a.scale_log2 = scale * kLog2e;
   a.out_f32 = out_dtype == AKV_F32;
   a.group = q_heads / kv_heads;
-  while ((1 << a.group_shift) < a.group) ++a.group_shift;  // the group divides 128: a power of two
-  a.tokens_per_block = rows_per_block(head_dim) / a.group;
+  while ((1 << a.group_shift) < a.group) ++a.group_shift;  // rows per token: the group padded to 2^shift
+  const int tile_dim = head_dim > 64 ? 128 : 64;
+  a.tokens_per_block = rows_per_block(tile_dim) >> a.group_shift;
+  a.head_dim = head_dim;
+  a.cap = logit_cap;
+  a.cap_log2 = logit_cap * kLog2e;
   const int64_t blocks = (max_query_len + a.tokens_per_block - 1) / a.tokens_per_block;
   if (blocks * kv_heads > 0x7fffffffLL) return fail(AKV_EINVAL, "akv_context_attention: queries too long");
   a.kv_heads = kv_heads;

@@ -387,11 +387,13 @@ int akv_decode_attention_noalloc(const void* q, int64_t q_stride_b,
  * positions from q_positions / kv_positions (both or neither; without them
  * q_pos = prefix_len + i, k_pos = j).  Positions ascend within a segment.
  * sinks (opt.) f32 [q_heads] add e^sink to the softmax denominator.
+ * logit_cap > 0 caps every scaled score s to logit_cap * tanh(s / logit_cap)
+ * before the softmax (0 = no cap).
  * q [Nq, q_heads, D], k_ext/v_ext [Nq, kv_heads, D], pool [slots, kv_heads, D]
- * bf16 with unit dim stride; out bf16 or f32 like q; D = 64 or 128;
- * q_heads / kv_heads divides 128, q_heads < 32768; scale > 0.  indptrs /
- * indices / positions: AKV_I32 or AKV_I64.  max_query_len: host bound on
- * every segment's query count.
+ * bf16 with unit dim stride; out bf16 or f32 like q; D a multiple of 8 up
+ * to 128; q_heads a multiple of kv_heads with at most 128 q heads per KV
+ * head, q_heads < 32768; scale > 0.  indptrs / indices / positions: AKV_I32
+ * or AKV_I64.  max_query_len: host bound on every segment's query count.
  * Replaces the Triton extend attention launched by
  * ContextAttentionMetadata.forward with context positions,
  * akv/system/sglang/srt/layers/attention/context_backend.py:180-251 and
@@ -411,9 +413,10 @@ int akv_context_attention(const void* q, int64_t q_stride_t,
                           int32_t indices_dtype, const void* q_positions,
                           const void* kv_positions, int32_t positions_dtype,
                           int32_t sliding_window, const float* sinks,
-                          float scale, void* out, int32_t out_dtype,
-                          int64_t out_stride_t, int64_t out_stride_h,
-                          int64_t max_query_len, void* stream);
+                          float scale, float logit_cap, void* out,
+                          int32_t out_dtype, int64_t out_stride_t,
+                          int64_t out_stride_h, int64_t max_query_len,
+                          void* stream);
 
 /*
  * Host (CPU) occurrence window of one forward: the (raw token, position)

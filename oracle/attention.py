@@ -46,7 +46,7 @@ def decode_attention(q, keys, values, scale, sinks=None):
 
 
 def context_attention(q, k_ext, v_ext, k_pool, v_pool, qo_indptr, kv_indptr, kv_indices, scale, *,
-                      window=-1, q_positions=None, kv_positions=None, sinks=None):
+                      window=-1, q_positions=None, kv_positions=None, sinks=None, logit_cap=0.0):
     """Prefill (extend) attention of context segments, in float64.
 
     Restates the extend attention with context positions
@@ -58,7 +58,10 @@ def context_attention(q, k_ext, v_ext, k_pool, v_pool, qo_indptr, kv_indptr, kv_
     ``window > 0`` a key is visible only when ``q_pos <= k_pos + window``
     (the extend kernel applies no window for 0 or less,
     ``akv/system/sglang.patch:527-541``); without positions
-    ``q_pos = prefix_length + i`` and prefix ``k_pos = j``.
+    ``q_pos = prefix_length + i`` and prefix ``k_pos = j``.  With
+    ``logit_cap > 0`` every scaled score ``s`` becomes
+    ``logit_cap * tanh(s / logit_cap)`` before the softmax (the extend
+    kernel's soft cap; sinks are not capped).
 
     ``q``: [Nq, Hq, D]; ``k_ext``/``v_ext``: [Nq, Hkv, D]; ``k_pool``/``v_pool``:
     [slots, Hkv, D].  Returns [Nq, Hq, D] float32.
@@ -97,6 +100,8 @@ def context_attention(q, k_ext, v_ext, k_pool, v_pool, qo_indptr, kv_indptr, kv_
             for h in range(hq):
                 g = h // group
                 sc = scale * (keys_k[vis, g, :] @ q[a + i, h])
+                if logit_cap > 0:
+                    sc = logit_cap * np.tanh(sc / logit_cap)
                 m = sc.max() if len(sc) else -np.inf
                 if sinks is not None:
                     m = max(m, float(sinks[h]))

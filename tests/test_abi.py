@@ -67,14 +67,24 @@ def test_validation_rejects_before_any_device_work(lib):
     assert lib.akv_write_extend_rows(*zeros(lib.akv_write_extend_rows)) == 0  # empty batch
     assert lib.akv_write_extend_rows(*zeros(lib.akv_write_extend_rows, a13=3)) == _lib.AKV_EINVAL
     assert "null device pointer" in _lib.last_error()
-    assert lib.akv_context_attention(*zeros(lib.akv_context_attention, a15=1, a17=1, a18=64, a34=4)) == _lib.AKV_EINVAL
+    assert lib.akv_context_attention(*zeros(lib.akv_context_attention, a15=1, a17=1, a18=64, a35=4)) == _lib.AKV_EINVAL
     # prefix indices without K/V pools: rejected instead of faulting on the
     # null pool (addresses are never dereferenced on this path)
     fake = 1 << 20
     args = zeros(lib.akv_context_attention, a0=fake, a3=fake, a4=fake, a15=1, a16=8, a17=1, a18=64, a19=fake,
-                 a20=fake, a22=fake, a29=0.125, a30=fake, a34=4)
+                 a20=fake, a22=fake, a29=0.125, a31=fake, a35=4)
     assert lib.akv_context_attention(*args) == _lib.AKV_EINVAL
     assert "without K/V pools" in _lib.last_error()
+    # head dims: multiples of 8 up to 128; at most 128 q heads per KV head;
+    # a logit cap is 0 or positive and finite
+    for a18, a16, a17, a30, message in [(60, 8, 1, 0.0, "head_dim 60"), (136, 8, 1, 0.0, "head_dim 136"),
+                                        (64, 129, 1, 0.0, "at most 128 per KV head"),
+                                        (64, 12, 8, 0.0, "at most 128 per KV head"),
+                                        (64, 8, 1, -1.0, "logit_cap"), (64, 8, 1, float("inf"), "logit_cap"),
+                                        (64, 8, 1, float("nan"), "logit_cap")]:
+        bad = zeros(lib.akv_context_attention, a15=1, a16=a16, a17=a17, a18=a18, a29=0.125, a30=a30, a35=4)
+        assert lib.akv_context_attention(*bad) == _lib.AKV_EINVAL
+        assert message in _lib.last_error(), (message, _lib.last_error())
     assert lib.akv_window_count(*zeros(lib.akv_window_count)) == _lib.AKV_EINVAL
     assert lib.akv_window_compile_bounded(*zeros(lib.akv_window_compile_bounded)) == _lib.AKV_EINVAL
     assert "null host pointer" in _lib.last_error()

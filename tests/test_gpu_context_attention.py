@@ -1,8 +1,9 @@
 """GPU parity of the prefill context attention (MFMA) against the float64
-oracle: ragged segments, empty and long prefixes, GQA groups 8 and 4, head
-dims 64 and 128, position-based sliding windows over positions with holes,
-the native (position-free) window, sinks, bf16 and f32 outputs; and batch
-metadata of plain requests bound to physical slots."""
+oracle: ragged segments, empty and long prefixes, GQA groups 8 and 4 and
+groups that are not powers of two, head dims 64 and 128 and narrower ones
+(multiples of 8), logit caps, position-based sliding windows over positions
+with holes, the native (position-free) window, sinks, bf16 and f32 outputs;
+and batch metadata of plain requests bound to physical slots."""
 
 import numpy as np
 import pytest
@@ -46,7 +47,7 @@ def _case(device, hq, hkv, d, q_lens, p_lens, seed, slots=4000):
     return dict(q=q, ke=ke, ve=ve, kp=kp, vp=vp, qo=qo, kv=kv, idx=idx, kpos=kpos, qpos=qpos, dev=dev)
 
 
-def _run(device, c, *, window, positions, sinks, out_dtype, scale):
+def _run(device, c, *, window, positions, sinks, out_dtype, scale, logit_cap=0.0):
     dv = c["dev"]
     out = torch.full(dv["q"].shape, 7.0, dtype=out_dtype, device=device)
     qo = torch.from_numpy(c["qo"]).to(device)
@@ -55,15 +56,46 @@ def _run(device, c, *, window, positions, sinks, out_dtype, scale):
     qp = torch.from_numpy(c["qpos"]).to(device) if positions else None
     kp = torch.from_numpy(c["kpos"]).to(device) if positions else None
     ca.extend_attention_fwd(dv["q"], dv["ke"], dv["ve"], out, dv["kp"], dv["vp"], qo, kv, idx, None, True, None,
-                            int(np.diff(c["qo"]).max()), sm_scale=scale, sliding_window_size=window, sinks=sinks,
-                            context_q_positions=qp, context_kv_positions=kp)
+                            int(np.diff(c["qo"]).max()), sm_scale=scale, logit_cap=logit_cap,
+                            sliding_window_size=window, sinks=sinks, context_q_positions=qp, context_kv_positions=kp)
     torch.cuda.synchronize()
     want = oat.context_attention(_f32(c["q"]), _f32(c["ke"]), _f32(c["ve"]), _f32(c["kp"]), _f32(c["vp"]),
                                  c["qo"], c["kv"], c["idx"], scale, window=window,
                                  q_positions=c["qpos"] if positions else None,
                                  kv_positions=c["kpos"] if positions else None,
-                                 sinks=_f32(sinks) if sinks is not None else None)
+                                 sinks=_f32(sinks) if sinks is not None else None, logit_cap=logit_cap)
     return _f32(out), want
+
+
+# groups that are not powers of two (padded rows), heads narrower than the
+# 64- / 128-dim tiles, logit caps, alone and together, with windows and sinks
+@pytest.mark.parametrize("d,hq,hkv,cap", [
+    (128, 28, 4, 0.0), (64, 12, 4, 0.0), (64, 40, 8, 0.0), (128, 7, 7, 0.0),
+    (80, 8, 8, 0.0), (96, 16, 2, 0.0), (32, 8, 1, 0.0), (112, 6, 2, 0.0), (8, 4, 4, 0.0),
+    (64, 64, 8, 30.0), (128, 32, 8, 5.0), (96, 24, 8, 20.0), (64, 6, 1, 2.0),
+])
+@pytest.mark.parametrize("window,positions,with_sinks", [(-1, False, False), (24, True, True)])
+def test_groups_head_dims_and_caps(device, d, hq, hkv, cap, window, positions, with_sinks):
+    c = _case(device, hq, hkv, d, Q_LENS, P_LENS, seed=3 * d + hq + int(cap) + window)
+    sinks = (torch.randn(hq, generator=torch.Generator().manual_seed(2)) * 2).to(device) if with_sinks else None
+    print(f"context attention d={d} hq={hq} hkv={hkv} cap={cap} window={window} sinks={with_sinks}", flush=True)
+    got, want = _run(device, c, window=window, positions=positions, sinks=sinks, out_dtype=torch.float32,
+                     scale=d ** -0.5, logit_cap=cap)
+    for s in range(len(Q_LENS)):
+        a, b = c["qo"][s], c["qo"][s + 1]
+        err = np.abs(got[a:b] - want[a:b]).max()
+        assert err <= TOL, f"segment {s} (q {Q_LENS[s]}, prefix {P_LENS[s]}) max err {err}"
+
+
+def test_capped_scores_far_apart(device):
+    """Capped logits with the scores spread ~50x the cap: the softmax sees
+    values in [-cap, cap] only, whatever Q and K hold."""
+    c = _case(device, 16, 4, 64, [70, 300], [500, 40], seed=77)
+    c["q"] = c["q"] * 8
+    c["dev"]["q"] = c["q"].to(device)
+    got, want = _run(device, c, window=-1, positions=False, sinks=None, out_dtype=torch.float32, scale=0.125,
+                     logit_cap=3.0)
+    assert np.abs(got - want).max() <= TOL
 
 
 Q_LENS = [1, 15, 16, 17, 100, 300, 5]

@@ -155,3 +155,43 @@ def test_context_sinks_scale_by_sigmoid_of_lse():
         lse = torch.logsumexp(torch.from_numpy(s), dim=1).numpy()
         want = base[i] * torch.sigmoid(torch.from_numpy(lse - sinks)).numpy()[:, None]
         np.testing.assert_allclose(got[i], want, atol=1e-6, rtol=1e-5)
+
+
+def test_context_logit_cap_equals_sdpa_on_capped_keys():
+    """A soft cap is a per-score transform.  With queries that read one key
+    dimension only (q = a e0), each score is scale * a * k[0]; uncapped
+    attention over keys whose first dim is replaced by
+    cap * tanh(scale * a * k[0] / cap) / (scale * a) (numpy's tanh) has
+    exactly the capped scores, so SDPA over those keys is the capped
+    oracle's answer.  Scores spread over +-40 against caps of 5 and 30, so a
+    cap on the unscaled score, a cap without the outer factor or none at all
+    all fail."""
+    rng = np.random.default_rng(12)
+    hq = hkv = 2
+    d = 8
+    q_lens, p_lens = [6, 1, 9], [5, 0, 13]
+    q, ke, ve, kp, vp, qo, kv, idx = _segments(rng, hq, hkv, d, q_lens, p_lens)
+    amp = np.array([1.5, -2.0])
+    q[:] = 0.0
+    q[:, :, 0] = amp[None, :]
+    ke[:, :, 0] = rng.uniform(-60, 60, size=ke.shape[:2])
+    kp[:, :, 0] = rng.uniform(-60, 60, size=kp.shape[:2])
+    scale = 0.45
+    for cap in (5.0, 30.0):
+        got = at.context_attention(q, ke, ve, kp, vp, qo, kv, idx, scale, logit_cap=cap)
+        for s in range(len(q_lens)):
+            a, b, x, y = qo[s], qo[s + 1], kv[s], kv[s + 1]
+            n, plen = b - a, y - x
+            keys = np.concatenate((kp[idx[x:y]], ke[a:b])).astype(np.float64)
+            vals = np.concatenate((vp[idx[x:y]], ve[a:b])).astype(np.float64)
+            mask = np.zeros((n, plen + n), dtype=bool)
+            mask[:, :plen] = True
+            mask[:, plen:] = np.tril(np.ones((n, n), dtype=bool))
+            for h in range(hq):
+                capped = keys.copy()
+                sc = scale * amp[h] * keys[:, h, 0]
+                capped[:, h, 0] = cap * np.tanh(sc / cap) / (scale * amp[h])
+                want = _sdpa(q[a:b, h : h + 1], capped[:, h : h + 1], vals[:, h : h + 1], mask, scale)
+                np.testing.assert_allclose(got[a:b, h : h + 1], want, atol=1e-6, rtol=1e-5)
+        uncapped = at.context_attention(q, ke, ve, kp, vp, qo, kv, idx, scale)
+        assert np.abs(got - uncapped).max() > 1e-2
