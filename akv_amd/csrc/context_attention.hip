@@ -136,10 +136,6 @@ __device__ __forceinline__ u32x4 load16(const __bf16* p) {
   return *((const global_u32x4*)p);
 }
 
-__device__ __forceinline__ u32x4 load16b(const char* p) {
-  return *((const global_u32x4*)p);
-}
-
 // One of the two LDS tile buffers.  They are separate objects, named
 // statically in each half of the unrolled tile loop, so the compiler sees
 // that this tile's LDS reads never touch the other buffer that the next

@@ -9,10 +9,13 @@
 // source bits; K dims [R, D) and all of V are copied bit for bit.
 //
 // MI355X design (not the reference's one-program-per-(token, layer, head)
-// grid): one workgroup per moved token walks every layer of the group, so the
-// token's slots and positions are read once and its cos/sin rows (with
-// cos^2 + sin^2) are staged once in LDS instead of being reloaded for every
-// (layer, head).  Each lane owns one "rotary unit" of a head: for NeoX style
+// grid): a workgroup moves the rows of about 256 threads' worth of
+// consecutive tokens (8 tokens of the 8 x 64 head layout) in one layer, with
+// the tokens' cos/sin rows (and cos^2 + sin^2) staged once in LDS for every
+// head.  Workgroups sweep token blocks fastest, then layers, in one sweep or
+// in token chunks (see the launch geometry below); token blocks come in
+// multiples of 8 so that a block meets the same XCD in every layer.  Each
+// lane owns one "rotary unit" of a head: for NeoX style
 // the 16-byte chunk at i and its partner chunk at i + R/2, so both halves of
 // every pair sit in the same lane and no cross-lane exchange is needed; for
 // GPT-J style one 16-byte chunk of interleaved pairs.  K and V move as 16-byte
@@ -20,8 +23,6 @@
 // instruction for the 8 x 64 bf16 head layout.  Layers whose base address is
 // not 16-byte aligned take an element-wise path inside the same kernel; other
 // shapes go to a generic element-per-thread kernel.
-#include <atomic>
-
 #include "common.h"
 
 namespace akv {
@@ -40,13 +41,13 @@ struct RepositionArgs {
   int32_t n_layers, n_heads, head_dim, rotary_dim;
   int32_t skip_unmapped;
   int32_t is_neox;
-  int32_t units_per_head;  // rotary units per head
-  int32_t lanes_per_row;   // n_heads * units_per_head
-  int32_t rows_per_block;  // layers processed side by side by one token
-  int32_t tokens_per_block;
-  int64_t whole_tokens;    // tokens [0, whole_tokens) take one workgroup over
-                           // every layer; each later token one workgroup per
-                           // rows_per_block layers (one token per workgroup)
+  int32_t units_per_head;    // rotary units per head
+  int32_t lanes_per_row;     // n_heads * units_per_head
+  int32_t tokens_per_block;  // consecutive tokens side by side in a workgroup
+  int32_t layers_per_block;  // layers a workgroup walks, one row per token at a time
+  int32_t layer_groups;      // ceil(n_layers / layers_per_block)
+  int32_t token_blocks;      // token blocks, rounded up to a multiple of 8
+  int32_t chunk_blocks;      // token blocks per chunk (a multiple of 8)
   int64_t n_tokens;
 };
 
@@ -196,6 +197,7 @@ struct RowData {
 // tail loops.
 template <typename T, typename CS, bool NEOX, bool WIDE>
 struct RowMover {
+  using Table = CS;
   static constexpr int VEC = Elem<T>::kVec;
   static constexpr int NP = NEOX ? VEC : VEC / 2;  // rotation pairs per lane
   const RepositionArgs& a;
@@ -222,9 +224,15 @@ struct RowMover {
 
   template <bool ALIGNED>
   __device__ __forceinline__ RowData load(int layer) const {
+    return load_at<ALIGNED>(a.k_ptrs[layer], a.v_ptrs[layer]);
+  }
+
+  // the rows of the layer whose K and V buffers start at kbase / vbase
+  template <bool ALIGNED>
+  __device__ __forceinline__ RowData load_at(uint64_t kbase, uint64_t vbase) const {
     RowData r;
-    r.kb = reinterpret_cast<char*>(static_cast<uintptr_t>(a.k_ptrs[layer]));
-    r.vb = reinterpret_cast<char*>(static_cast<uintptr_t>(a.v_ptrs[layer]));
+    r.kb = reinterpret_cast<char*>(static_cast<uintptr_t>(kbase));
+    r.vb = reinterpret_cast<char*>(static_cast<uintptr_t>(vbase));
     r.k1 = load16<ALIGNED>(at(r.kb, k_src, ko1));
     r.k2 = NEOX ? load16<ALIGNED>(at(r.kb, k_src, ko2)) : make_u32x4(0, 0, 0, 0);
     // without a K tail a NeoX lane moves exactly two V units and a GPT-J lane
@@ -310,88 +318,112 @@ struct RowMover {
   }
 };
 
-// Workgroup = tokens_per_block tokens x rows_per_block layer rows side by
-// side x lanes_per_row lanes; each lane walks the layers of its token, one
-// row per pass (load, then rotate and store).  Dynamic LDS holds, per token,
-// the five coefficient arrays of its `half` frequencies.
+// The rows of one token over layers [lbeg, lend): the first layer's K/V
+// rows and the token's table rows are loaded together (one round trip), the
+// coefficients go to LDS, the one barrier publishes them (waiting for the
+// LDS stores only, not for the rows in flight), then each layer is rotated
+// and stored, one row in flight per lane (measured faster than prefetching
+// the next layer's row: fewer registers, more resident waves).  The loads
+// are unconditional -- a lane with no live token reads slot 0's row and
+// table row 0, which every pool and table has -- so no load waits behind a
+// divergent branch; only the stores are predicated.  Every thread of the
+// workgroup reaches the barrier.
+template <bool ALIGNED, typename Mover>
+__device__ __forceinline__ void move_rows(const RepositionArgs& a, Mover& mv, float* coef, int cstride, int half,
+                                          int j, int lpr, bool rotating, bool moving, int64_t old_pos,
+                                          int64_t new_pos, int lbeg, int lend, uint64_t kbase, uint64_t vbase) {
+  using CS = typename Mover::Table;
+  const RowData row = mv.template load_at<ALIGNED>(kbase, vbase);
+  const CS* table = static_cast<const CS*>(a.cos_sin);
+  const CS* ro = table + (rotating ? old_pos : 0) * a.rope_stride;
+  const CS* rn = table + (rotating ? new_pos : 0) * a.rope_stride;
+  for (int f = j; f < half; f += lpr) {
+    const float co = to_float(ro[f]);
+    const float so = to_float(ro[half + f]);
+    const float cn = to_float(rn[f]);
+    const float sn = to_float(rn[half + f]);
+    if (rotating) {
+      coef[f] = co;
+      coef[cstride + f] = so;
+      coef[2 * cstride + f] = cn;
+      coef[3 * cstride + f] = sn;
+      coef[4 * cstride + f] = co * co + so * so;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  if (!moving) return;
+  mv.template finish<ALIGNED>(row);
+  for (int layer = lbeg + 1; layer < lend; ++layer) mv.template finish<ALIGNED>(mv.template load<ALIGNED>(layer));
+}
+
+// Workgroup = tokens_per_block consecutive tokens x lanes_per_row lanes, over
+// layers_per_block layers of one layer group (token inner: a wave covers
+// consecutive tokens of one layer, so slot-adjacent tokens make one
+// contiguous span).  Token blocks are numbered fastest, so at any moment the
+// device works through a few layers' buffers.  Dynamic LDS holds, per
+// token, the five coefficient arrays of its `half` frequencies.  One round
+// trip brings the token's list entries, the gate and the layer bases, the
+// next both its table rows and its first layer's K/V rows; only the LDS
+// coefficients wait at the barrier.
 template <typename T, typename CS, bool NEOX, bool WIDE>
 __global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionArgs a) {
   using Mover = RowMover<T, CS, NEOX, WIDE>;
   constexpr int VEC = Mover::VEC;
   extern __shared__ float4 coef_lds[];
   const int lpr = a.lanes_per_row;
-  const int row_threads = lpr * a.rows_per_block;
-  const int slot = threadIdx.x / row_threads;
-  const int local = threadIdx.x - slot * row_threads;
-  const int row_sub = local / lpr;
-  const int j = local - row_sub * lpr;
-  // the launch's last tokens are cut into one workgroup per group of
-  // rows_per_block layers, so its tail is made of short workgroups
-  int64_t token;
-  int lbeg = 0, lend = a.n_layers;
-  if (static_cast<int64_t>(blockIdx.x) < a.whole_tokens || a.tokens_per_block != 1) {
-    token = static_cast<int64_t>(blockIdx.x) * a.tokens_per_block + slot;
-  } else {
-    const int parts = (a.n_layers + a.rows_per_block - 1) / a.rows_per_block;
-    const int64_t u = static_cast<int64_t>(blockIdx.x) - a.whole_tokens;
-    token = a.whole_tokens + u / parts;
-    lbeg = static_cast<int>(u % parts) * a.rows_per_block;
-    lend = lbeg + a.rows_per_block < a.n_layers ? lbeg + a.rows_per_block : a.n_layers;
+  const int slot = threadIdx.x / lpr;
+  const int j = threadIdx.x - slot * lpr;
+  // workgroup -> (chunk, layer group, token block), token blocks fastest
+  const uint32_t per_chunk = static_cast<uint32_t>(a.chunk_blocks) * static_cast<uint32_t>(a.layer_groups);
+  const uint32_t full = static_cast<uint32_t>(a.token_blocks / a.chunk_blocks);
+  uint32_t r, rb, first;
+  if (blockIdx.x < full * per_chunk) {
+    const uint32_t chunk = blockIdx.x / per_chunk;
+    r = blockIdx.x - chunk * per_chunk;
+    rb = static_cast<uint32_t>(a.chunk_blocks);
+    first = chunk * rb;
+  } else {  // the last, shorter chunk
+    r = blockIdx.x - full * per_chunk;
+    first = full * static_cast<uint32_t>(a.chunk_blocks);
+    rb = static_cast<uint32_t>(a.token_blocks) - first;
   }
+  const uint32_t group = r / rb;
+  const int64_t token = static_cast<int64_t>(first + (r - group * rb)) * a.tokens_per_block + slot;
+  // group < ceil(n_layers / layers_per_block): the layer range is never empty
+  const int lbeg = static_cast<int>(group) * a.layers_per_block;
+  const int lend = lbeg + a.layers_per_block < a.n_layers ? lbeg + a.layers_per_block : a.n_layers;
   const int half = a.rotary_dim >> 1;
   const int cstride = coef_stride(half);
   float* coef = reinterpret_cast<float*>(coef_lds) + slot * 5 * cstride;
 
-  // every thread reaches the barrier below: a token past the end or an
-  // unmapped one only skips its work
+  // one round of independent loads: the gate, the layer bases and the
+  // token's list entries (lanes past the end read the last token's entries)
+  // (without a gate the load reads the first source slot, any word will do)
+  const int32_t word = __hip_atomic_load(a.gate ? a.gate : a.src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t kbase = a.k_ptrs[lbeg], vbase = a.v_ptrs[lbeg];
+  const int64_t tc = token < a.n_tokens ? token : a.n_tokens - 1;
+  const int64_t src = a.src[tc];
+  const int64_t dst = a.dst[tc];
+  const int32_t* pair = a.pairs + tc * a.pair_stride;
+  const int64_t old_pos = pair[0];
+  const int64_t new_pos = pair[1];
+  // every load above is issued before anything waits for one of them (the
+  // scheduler would otherwise test the gate first): one round trip.  A
+  // closed gate then stops the whole workgroup (the word is the same for
+  // every thread) before any K/V row or table row is read.
+  __builtin_amdgcn_sched_barrier(0);
+  if (a.gate && (word & AKV_STATUS_UNUSABLE) != 0) return;
+  const bool live = token < a.n_tokens && !(a.skip_unmapped && (src <= 0 || dst <= 0));
   Mover mv{a};
-  bool live = token < a.n_tokens;
-  int64_t src = 0, dst = 0, old_pos = 0, new_pos = 0;
-  if (live) {
-    src = a.src[token];
-    dst = a.dst[token];
-    live = !(a.skip_unmapped && (src <= 0 || dst <= 0));
-    const int32_t* pair = a.pairs + token * a.pair_stride;
-    old_pos = pair[0];
-    new_pos = pair[1];
-  }
-  // the gate is read with the token's list entries; a closed gate stops the
-  // token before its table rows and K/V rows are touched
-  if (gated(a.gate)) live = false;
   mv.same = old_pos == new_pos;
-  if (live && !mv.same) {
-    const CS* table = static_cast<const CS*>(a.cos_sin);
-    const CS* ro = table + old_pos * a.rope_stride;
-    const CS* rn = table + new_pos * a.rope_stride;
-    for (int f = local; f < half; f += row_threads) {
-      const float co = to_float(ro[f]);
-      const float so = to_float(ro[half + f]);
-      coef[f] = co;
-      coef[cstride + f] = so;
-      coef[2 * cstride + f] = to_float(rn[f]);
-      coef[3 * cstride + f] = to_float(rn[half + f]);
-      coef[4 * cstride + f] = co * co + so * so;
-    }
-  }
-  // one 16-byte-unaligned layer base sends the whole workgroup down the
-  // element-wise path (a uniform branch): the first wave takes the vote and
-  // publishes it in LDS before the one barrier
-  __shared__ int any_misaligned;
-  const int first_wave = blockDim.x < 64 ? static_cast<int>(blockDim.x) : 64;
-  if (static_cast<int>(threadIdx.x) < first_wave) {
-    bool bad = false;
-    for (int l = threadIdx.x; l < a.n_layers; l += first_wave) bad |= ((a.k_ptrs[l] | a.v_ptrs[l]) & 15) != 0;
-    const bool any = __ballot(bad) != 0;
-    if (threadIdx.x == 0) any_misaligned = any;
-  }
-  __syncthreads();
-  const bool aligned = !any_misaligned;
-  if (!live || lbeg + row_sub >= lend) return;
+  const bool rotating = live && !mv.same;
 
   constexpr int64_t B = sizeof(T);
-  mv.k_src = src * a.k_stride_slot * B;
+  mv.k_src = (live ? src : 0) * a.k_stride_slot * B;
   mv.k_dst = dst * a.k_stride_slot * B;
-  mv.v_src = src * a.v_stride_slot * B;
+  mv.v_src = (live ? src : 0) * a.v_stride_slot * B;
   mv.v_dst = dst * a.v_stride_slot * B;
   mv.lpr = lpr;
   mv.j = j;
@@ -409,15 +441,16 @@ __global__ void __launch_bounds__(1024) reposition_vec_kernel(const RepositionAr
   mv.vo1 = static_cast<int32_t>((vh1 * a.v_stride_head + (c1 - vh1 * v_units_head) * VEC) * B);
   mv.coef = coef + (NEOX ? g * VEC : g * (VEC / 2));
   mv.cstride = cstride;
-  // one row in flight per lane: measured faster than prefetching the next
-  // layer's row (fewer registers, more resident waves)
-  if (aligned) {
-    for (int layer = lbeg + row_sub; layer < lend; layer += a.rows_per_block)
-      mv.template finish<true>(mv.template load<true>(layer));
-  } else {
-    for (int layer = lbeg + row_sub; layer < lend; layer += a.rows_per_block)
-      mv.template finish<false>(mv.template load<false>(layer));
-  }
+
+  // the workgroup's layers share one form: 16-byte vectors when every base
+  // is 16-byte aligned, else element-wise (a uniform branch around the rest)
+  bool aligned = ((kbase | vbase) & 15) == 0;
+  for (int layer = lbeg + 1; layer < lend; ++layer) aligned &= ((a.k_ptrs[layer] | a.v_ptrs[layer]) & 15) == 0;
+  if (aligned)
+    move_rows<true>(a, mv, coef, cstride, half, j, lpr, rotating, live, old_pos, new_pos, lbeg, lend, kbase, vbase);
+  else
+    move_rows<false>(a, mv, coef, cstride, half, j, lpr, rotating, live, old_pos, new_pos, lbeg, lend, kbase,
+                     vbase);
 }
 
 // Any layout: one thread per (token, layer, head, dim) element.
@@ -474,43 +507,29 @@ __global__ void __launch_bounds__(256) reposition_generic_kernel(const Repositio
   }
 }
 
-// Launch geometry of the vector kernel.  Measured on MI355X for the
-// 36-layer x 8-head x 64 bf16 shape (32 lanes per row): about 384 threads
-// per token (12 layers side by side, 3 passes, one row in flight per lane)
-// beat 192 threads with the next layer prefetched, 576 threads, and several
-// tokens per workgroup; tokens whose rows fill less than two waves share a
-// workgroup.
-constexpr int kMaxDevices = 64;
-
+// Launch geometry of the vector kernel, measured on MI355X for the 36-layer
+// x 8-head x 64 bf16 shape (32 lanes per row) over random and ascending
+// slots: 8 tokens x 1 layer per 256-thread workgroup (token blocks fastest)
+// beat the earlier 1 token x 36 layers (12 side by side, 3 passes) by 1-1.5%
+// on random slots and 7% on ascending ones, and beat 2-32 tokens x 1-4
+// layers, several layers side by side, layer groups fastest, and lanes
+// reading their coefficients straight from the table instead of LDS.  The
+// rule: about 256 threads of consecutive tokens, one layer each.
+// The sweep order, measured on MI355X: every layer's workgroup re-reads its
+// tokens' cos/sin rows (25% over the K/V reads of a GPT-OSS row), which
+// stays cheap while the rows of all tokens stay cached.  So one sweep when
+// they fit kSweepTableBytes (the 32k GPT-OSS request's 12064 copies: 6 MB;
+// chunks of 4096-12288 tokens measured 0.5-1.5% slower), else chunks of
+// kChunkTokens tokens, each swept over every layer before the next (Llama-3
+// page-16 copy-on-write, 777k copies and 777 MB of table rows: 61% of HBM
+// peak in one sweep, 72 / 75 / 76.7% in chunks of 16384 / 4096 / 1024).
+constexpr int64_t kSweepTableBytes = 16ll << 20;
+constexpr int64_t kChunkTokens = 1024;
 void geometry(RepositionArgs& a) {
-  const int lpr = a.lanes_per_row;
-  int rows = 384 / lpr;
-  if (rows < 1) rows = 1;
-  if (rows > a.n_layers) rows = a.n_layers;
-  const int passes = (a.n_layers + rows - 1) / rows;
-  rows = (a.n_layers + passes - 1) / passes;  // balance the passes
-  while (rows > 1 && rows * lpr > 1024) --rows;
-  a.rows_per_block = rows;
-  int tokens = 128 / (rows * lpr);
+  int tokens = 256 / a.lanes_per_row;
   if (tokens < 1) tokens = 1;
-  while (tokens > 1 && tokens * rows * lpr > 1024) --tokens;
   a.tokens_per_block = tokens;
-}
-
-// Workgroups of `kernel` resident at once on the current device (0 when the
-// query fails), cached per device in `cache`.
-int64_t resident_workgroups(const void* kernel, int threads, size_t lds, std::atomic<int64_t>* cache) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-  int64_t c = cache[dev].load(std::memory_order_relaxed);
-  if (c > 0) return c;
-  int blocks = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, threads, lds) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 0;
-  c = static_cast<int64_t>(blocks) * cus;
-  cache[dev].store(c, std::memory_order_relaxed);
-  return c;
+  a.layers_per_block = 1;
 }
 
 template <typename T, typename CS>
@@ -521,27 +540,28 @@ int launch_typed(RepositionArgs a, int64_t n_tokens, hipStream_t stream, bool ve
     a.units_per_head = a.is_neox ? a.rotary_dim / (2 * VEC) : a.rotary_dim / VEC;
     a.lanes_per_row = a.n_heads * a.units_per_head;
     geometry(a);
-    const int threads = a.lanes_per_row * a.rows_per_block * a.tokens_per_block;
+    const int threads = a.lanes_per_row * a.tokens_per_block;
     const size_t lds = static_cast<size_t>(a.tokens_per_block) * 5 * coef_stride(a.rotary_dim >> 1) * sizeof(float);
     const bool wide = a.rotary_dim < a.head_dim || a.n_heads * (a.head_dim / VEC) > 2 * a.lanes_per_row;
     void (*kernel)(RepositionArgs) =
         a.is_neox ? (wide ? reposition_vec_kernel<T, CS, true, true> : reposition_vec_kernel<T, CS, true, false>)
                   : (wide ? reposition_vec_kernel<T, CS, false, true> : reposition_vec_kernel<T, CS, false, false>);
-    // the last tokens -- one device-full of workgroups -- each take one
-    // workgroup per pass, so the launch does not end on a partial round of
-    // full-length workgroups
-    int64_t units = (n_tokens + a.tokens_per_block - 1) / a.tokens_per_block;
-    a.whole_tokens = n_tokens;
-    const int parts = (a.n_layers + a.rows_per_block - 1) / a.rows_per_block;
-    if (a.tokens_per_block == 1 && parts > 1) {
-      static std::atomic<int64_t> cache[2][2][kMaxDevices];
-      int64_t tail = resident_workgroups(reinterpret_cast<const void*>(kernel), threads, lds,
-                                         cache[a.is_neox ? 1 : 0][wide ? 1 : 0]);
-      if (tail > n_tokens) tail = n_tokens;
-      a.whole_tokens = n_tokens - tail;
-      units = a.whole_tokens + tail * parts;
-    }
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(units)), dim3(threads), lds, stream, a);
+    // token blocks in multiples of 8: the dispatcher deals workgroups to the
+    // 8 XCDs round robin, so a token block meets the same XCD (and L2) in
+    // every layer (the padding blocks hold no live token)
+    const int64_t blocks = ((n_tokens + a.tokens_per_block - 1) / a.tokens_per_block + 7) / 8 * 8;
+    const int64_t groups = (a.n_layers + a.layers_per_block - 1) / a.layers_per_block;
+    const int64_t table_bytes = n_tokens * 2 * a.rotary_dim * static_cast<int64_t>(sizeof(CS));
+    const int64_t chunk_tokens = table_bytes <= kSweepTableBytes ? n_tokens : kChunkTokens;
+    int64_t chunk = ((chunk_tokens + a.tokens_per_block - 1) / a.tokens_per_block + 7) / 8 * 8;
+    if (chunk > blocks) chunk = blocks;
+    if (blocks * groups > 0x7fffffffLL)
+      return fail(AKV_EINVAL, "akv_reposition_kv_layers: %lld tokens x %d layers exceed one launch",
+                  static_cast<long long>(n_tokens), a.n_layers);
+    a.token_blocks = static_cast<int32_t>(blocks);
+    a.chunk_blocks = static_cast<int32_t>(chunk);
+    a.layer_groups = static_cast<int32_t>(groups);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks * groups)), dim3(threads), lds, stream, a);
     return check_launch("akv_reposition_kv_layers");
   }
   const int64_t total = n_tokens * a.n_layers * a.n_heads * a.head_dim;
