@@ -1,8 +1,9 @@
 """GPU parity of the fused Reposition kernel against the CPU oracle.
 
 Bit-exact for K, V and every untouched slot, across dtypes, pair styles,
-partial rotary widths, strides, pointer alignment and the full 32k GPT-OSS
-shape (sampled oracle check + size-independent properties at full size).
+partial rotary widths, strides, pointer alignment, lists long enough to be
+swept in token chunks, and the full 32k GPT-OSS shape (every destination
+row of every layer against the torch-CPU restatement).
 """
 
 import re
@@ -99,9 +100,10 @@ def test_partial_rotary(device, rotary_dim):
     _run_case(device, rotary_dim=rotary_dim, neox=False, seed=4)
 
 
-# (8, 128, 32) is the Llama-3 geometry (64 lanes per row, 3 layers side by
-# side, 11 passes with a short last pass); (4, 64, 36) one TP=2 rank's
-# GPT-OSS share (16 lanes per row, several tokens per workgroup)
+# (8, 64, 36) is the GPT-OSS geometry (32 lanes per row, 8 tokens per
+# workgroup); (8, 128, 32) the Llama-3 one (64 lanes per row, 4 tokens);
+# (4, 64, 36) one TP=2 rank's GPT-OSS share (16 lanes per row, 16 tokens);
+# (1, 16, 2) and (3, 32, 2) rows narrower than a wave
 @pytest.mark.parametrize("heads,head_dim,layers", [(8, 64, 36), (8, 128, 3), (8, 128, 32), (4, 64, 36), (4, 64, 5),
                                                    (1, 16, 2), (3, 32, 2)])
 def test_shapes(device, heads, head_dim, layers):
@@ -126,6 +128,17 @@ def test_exact_known_answers(device, neox):
     np.testing.assert_array_equal(to_storage(vt)[dst], v[0][src])
     untouched = np.setdiff1d(np.arange(len(got)), dst)
     np.testing.assert_array_equal(got[untouched], k[0][untouched])
+
+
+@pytest.mark.parametrize("heads,head_dim,layers,moved", [(8, 64, 4, 40003), (8, 128, 3, 17001)])
+def test_chunked_sweep(device, heads, head_dim, layers, moved):
+    """Lists whose cos/sin rows pass 16 MiB (32768 tokens of a 64-dim fp32
+    table, 16384 of a 128-dim one) are swept in 1024-token chunks: odd
+    counts leave a partial last block and padding blocks in the last, shorter
+    chunk.  Unmapped entries and same-position pairs mixed in."""
+    print(f"chunked sweep {heads}x{head_dim}, {layers} layers, {moved} tokens", flush=True)
+    _run_case(device, layers=layers, heads=heads, head_dim=head_dim, slots=2 * moved + 8, moved=moved, seed=11,
+              skip_unmapped=True, same_every=5)
 
 
 def test_skip_unmapped_and_same_position(device):
