@@ -1,7 +1,6 @@
 """GPU parity of the decode-attention consumer (MFMA) and the end-to-end
 decode check over Drop + Reposition metadata (GPT-OSS decode shape)."""
 
-import dataclasses
 
 import numpy as np
 import pytest
@@ -97,10 +96,13 @@ def test_random_batches_match_oracle(device, seed):
 
 
 def test_gpt_oss_decode_after_drop_and_reposition(device):
-    """32 requests x 32k tokens: compaction -> Reposition -> full / 128-window
-    metadata -> one decode step on a sliding-window and a full layer."""
+    """32 requests x 32k tokens: compaction -> Reposition of all 36 layers ->
+    full / 128-window metadata -> one decode step on every layer (GPT-OSS
+    alternates them: even layers sliding-window, odd layers full), each
+    checked against the oracle on four requests."""
     w = synth.workload("gpt-oss-decode-32x32k")
-    model = dataclasses.replace(w.model, n_layers=2)  # layer 0: window 128, layer 1: full
+    model = w.model
+    assert model.n_layers == 36
     layouts = synth.compile_layouts(w)
     slots = synth.assign_slots(w, layouts)
     B, n = w.n_requests, w.lengths[0]
@@ -137,10 +139,11 @@ def test_gpt_oss_decode_after_drop_and_reposition(device):
 
     g = torch.Generator().manual_seed(5)
     q = torch.randn((B, 64, 64), generator=g).to(torch.bfloat16).to(device)
-    sinks = [torch.randn(64, generator=g).to(device) for _ in range(2)]
+    sinks = [torch.randn(64, generator=g).to(device) for _ in range(model.n_layers)]
     outs = []
-    for layer, (ip, ix, mx) in enumerate(((win_indptr, win_idx, window + 1),
-                                          (out.kv_indptr, out.kv_indices, max(inputs.kept) + 1))):
+    for layer in range(model.n_layers):
+        ip, ix, mx = ((win_indptr, win_idx, window + 1) if layer % 2 == 0 else
+                      (out.kv_indptr, out.kv_indices, max(inputs.kept) + 1))
         o = torch.empty((B, 64, 64), dtype=torch.bfloat16, device=device)
         attention.decode_attention(q, pool.k[layer], pool.v[layer], ip, ix, o, scale=0.125, max_len=mx,
                                    sinks=sinks[layer], status=out.status)
@@ -162,9 +165,12 @@ def test_gpt_oss_decode_after_drop_and_reposition(device):
         np.testing.assert_array_equal(full_ix[full_ip[b] : full_ip[b + 1]], full)
         np.testing.assert_array_equal(win_ix[win_ip[b] : win_ip[b + 1]], visible)
         assert len(visible) == window + 1
-        for layer, keys in ((0, visible), (1, full)):
+        for layer in range(model.n_layers):
+            keys = visible if layer % 2 == 0 else full
             sel = torch.from_numpy(keys.astype(np.int64)).to(device)
             kk, vv = _f32(pool.k[layer][sel]), _f32(pool.v[layer][sel])
             want = oat.decode_attention(qq[b], kk, vv, 0.125, _f32(sinks[layer]))
             err = np.abs(_f32(outs[layer][b]) - want).max()
             assert err <= TOL, f"request {b} layer {layer}: max err {err}"
+    del pool, outs
+    torch.cuda.empty_cache()  # the 144 GiB pool
