@@ -895,7 +895,11 @@ constexpr int kMaxGroups = 32;
 constexpr int kSyncStride = 32;  // one 128-byte line per word
 constexpr uint32_t kCancelled = 0x80000000u;
 constexpr uint32_t kTagMask = 0x0fffffffu;
-constexpr uint32_t kPollLimit = 1u << 20;  // ~1 s of polling at most
+// polls of a bounded wait (one coherent load and a short sleep each: tens of
+// milliseconds in all, orders of magnitude above any wait at this barrier
+// when every tile is resident; a call whose tiles cannot all be resident
+// stalls this long before its fallback)
+constexpr uint32_t kPollLimit = 1u << 15;
 constexpr int64_t kFusedMaxTiles = static_cast<int64_t>(kGroupTiles) * kMaxGroups;
 // arrival counters, group records, release words, the epoch and the fail
 // word (one line each), then the groups' span start counts
