@@ -16,7 +16,9 @@ reduces to ``v e^s / (e^s + e^sink)``.
 causal SDPA (no prefix), SDPA with an explicit prefix-plus-causal mask, the
 reference's own windowed gather (``native_plan``: ``searchsorted`` of
 ``q_pos - window`` over the segment's ordered key positions, then plain
-attention per query, ``context_backend.py:196-238``), and the sink form.
+attention per query, ``context_backend.py:196-238``), and the sink form;
+its logit cap against SDPA over keys whose one score-carrying dimension
+holds the capped score (queries that read only that dimension).
 """
 
 import numpy as np
