@@ -45,6 +45,12 @@
 // key-major tile through ds_read_b64_tr_b16.  Tiles wholly inside every
 // row's causal and window range skip the mask.
 //
+// Two instances of each shape: the plain one (head_dim 64 or 128, the group
+// a power of two, no logit cap) and the general one, which pads a token's
+// rows to a power-of-two group (padding rows keep Q = 0 and store nothing),
+// runs heads narrower than the tile with the unloaded dims zero in LDS, and
+// caps scaled scores at cap tanh(s / cap) before the mask.
+//
 // Lane layouts (verified on gfx950): v_mfma_f32_16x16x32_bf16 -- lane l
 // supplies A[l%16][k(l,i)], B[k(l,i)][l%16] for i < 8 and holds
 // D[4(l/16)+i][l%16]; ds_read_b64_tr_b16 -- within each 16-lane group, lane
@@ -139,7 +145,9 @@ __device__ __forceinline__ u32x4 load16(const __bf16* p) {
 // One of the two LDS tile buffers.  They are separate objects, named
 // statically in each half of the unrolled tile loop, so the compiler sees
 // that this tile's LDS reads never touch the other buffer that the next
-// tile's direct loads are filling (no wait on those loads mid-tile).
+// tile's direct loads are filling (no wait on those loads mid-tile in the
+// 64-key instances; the rolled quarter loop of the 128-key ones still gets
+// a wait before its transposing reads, which measured free).
 template <int D, int KEYS>
 struct TileLds {
   __bf16 k[KEYS][D];   // key-major K tile, 16 B chunks swizzled per row (swz_k)
@@ -450,7 +458,10 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
       }
       if (cap) {
         // capped logits: cap tanh(scale s / cap), in the log2 domain, before
-        // the mask (a masked score stays -inf); tanh(x) = 1 - 2 / (1 + e^2x)
+        // the mask (a masked score stays -inf); tanh(x) = 1 - 2 / (1 + e^2x).
+        // The cap of SGLang's extend kernel, which the reference hands the
+        // layer's cap (akv/system/sglang.patch:2437,2459): scale, then cap.
+        // Sinks are not capped.
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll

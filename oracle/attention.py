@@ -62,8 +62,12 @@ def context_attention(q, k_ext, v_ext, k_pool, v_pool, qo_indptr, kv_indptr, kv_
     ``akv/system/sglang.patch:527-541``); without positions
     ``q_pos = prefix_length + i`` and prefix ``k_pos = j``.  With
     ``logit_cap > 0`` every scaled score ``s`` becomes
-    ``logit_cap * tanh(s / logit_cap)`` before the softmax (the extend
-    kernel's soft cap; sinks are not capped).
+    ``logit_cap * tanh(s / logit_cap)`` before the softmax; sinks are not
+    capped.  The cap is applied inside SGLang's extend-attention Triton
+    kernel (``sglang==0.5.20+akv``, upstream base commit 94602c9c,
+    ``akv/system/pyproject.toml:13,32``; not part of the reference tree),
+    which scales the score first and caps it second; the reference passes
+    the layer's cap to it at ``akv/system/sglang.patch:2437,2459``.
 
     ``q``: [Nq, Hq, D]; ``k_ext``/``v_ext``: [Nq, Hkv, D]; ``k_pool``/``v_pool``:
     [slots, Hkv, D].  Returns [Nq, Hq, D] float32.
