@@ -17,7 +17,10 @@
 // MI355X this measured ~4% faster than a workgroup per token walking its
 // layers, for the same random 1 KiB rows; with no slot vectors on either
 // side it is a streaming copy.  Longer rows: flat 16-byte work items,
-// kBatch independent loads in flight per thread.
+// kBatch independent loads in flight per thread.  Stores are nontemporal (a
+// copied row is not read back here): on MI355X the pack measured +8%, the
+// unpack and pool-to-pool copies +2%, the random-row gather +1.5-2% and the
+// streaming copy +3% against plain stores.
 #include "common.h"
 
 namespace akv {
@@ -75,7 +78,7 @@ __global__ void __launch_bounds__(kThreads) copy_kv_rows_kernel(const CopyArgs a
     }
 #pragma unroll
     for (int k = 0; k < kBatch; ++k)
-      if (dst[k]) *((global_u32x4*)dst[k]) = v[k];
+      if (dst[k]) __builtin_nontemporal_store(v[k], (global_u32x4*)dst[k]);
   }
 }
 
@@ -111,7 +114,7 @@ __global__ void __launch_bounds__(256) copy_rows_layer_major(const CopyArgs a, i
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     const int c = c0 + k * lanes;
-    if (c < a.chunks) *((global_u32x4*)(dst + 16 * c)) = v[k];
+    if (c < a.chunks) __builtin_nontemporal_store(v[k], (global_u32x4*)(dst + 16 * c));
   }
 }
 
