@@ -843,7 +843,8 @@ def ceiling_legs(pipe, steps, warmup, flush):
 
     Random slots (the workload's own lists):
     * gather copy: ``akv_copy_kv_rows`` of the same source -> destination K
-      and V rows of every layer (no arithmetic, one launch), in raw order,
+      and V rows of every layer (no arithmetic, one launch, stores
+      nontemporal like the Reposition's), in raw order,
       sorted by source slot and sorted by destination slot, each beside the
       Reposition with its lists in the same order;
     * torch's ``index_select`` / ``index_copy_`` over the same rows (kernels
@@ -876,7 +877,8 @@ def ceiling_legs(pipe, steps, warmup, flush):
     best = max([v for v in r["gather_copy_GBs"].values()] + list(r["torch"].values())
                + list(r["gather_copy_by_row_size_GBs"].values()))
     out["best_random_row_copy_pct_hbm_peak"] = round(100 * best / HBM_PEAK_GBS, 2)
-    out["kernel"] = "akv_copy_kv_rows (layer-major, one row per wave); torch index_select / index_copy_"
+    out["kernel"] = ("akv_copy_kv_rows (layer-major, one row per wave, nontemporal stores as in the "
+                     "Reposition); torch index_select / index_copy_")
     out["rounds"] = CEILING_ROUNDS
     return out
 
