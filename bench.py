@@ -1000,6 +1000,23 @@ def _chunked_ownership_port():
     return time.perf_counter() - t0
 
 
+def host_event_compile_ms(w, runs=5):
+    """Host time of the native event compile (``compile_context_layout``,
+    C++) for the workload's requests: median of ``runs`` warm runs."""
+    from akv_amd import plan as lp
+
+    events = [synth.request_events(n, spans) for n, spans in zip(w.lengths, w.spans)]
+    for e in events:
+        lp.compile_context_layout(**e)
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        for e in events:
+            lp.compile_context_layout(**e)
+        times.append(time.perf_counter() - t0)
+    return round(float(np.median(times)) * 1e3, 3)
+
+
 def compaction_passes(inputs):
     """Passes akv_compact_rows makes over this batch on this device: 1 (one
     kernel whose tiles meet at an in-kernel barrier) or 2 (count, scatter)."""
@@ -1190,6 +1207,9 @@ def main():
         "kernel_launches_per_step": 1 if args.reposition_only else compaction_launches(pipe.inputs) + 1,
         "compaction_passes": None if args.reposition_only else compaction_passes(pipe.inputs),
         "compaction_status": status,
+        # the request's Drop + Reposition events compiled on the host (C++),
+        # median of 5 warm runs: the CPU work before the step's launches
+        "host_event_compile_ms": host_event_compile_ms(pipe.w),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),
