@@ -1149,8 +1149,11 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(88)))
   const int64_t t1 = t0 + T::kTile < a.total ? t0 + T::kTile : a.total;
   const int n = a.n_requests;
   const int k = static_cast<int>(tile / kGroupTiles);
+  // the epoch goes to LDS only after the input loads are issued: stored at
+  // once, its load would hold wave 0's inputs back by a round trip
+  uint32_t epoch = 0;
   if (threadIdx.x == 0) {
-    s_sync[0] = load32(epoch_word(a));
+    epoch = load32(epoch_word(a));
     // status bit 1 until the last group's look-back completes
     if (tile == 0 && a.status) __hip_atomic_store(a.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -1161,13 +1164,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(88)))
   load_inputs<STEPS>(a, t0, t1, kb, bps, fps);
   load_birth_slots<STEPS>(a, t0, t1, slot0);
   stage_batch<STEPS>(a, sh);
+  if (threadIdx.x == 0) s_sync[0] = epoch;  // published by tile_masks' barriers
   const int64_t x[kWaves] = {t0 - 1, t1 - 1, t0, t1};
   tile_masks<STEPS, true>(a, sh, t0, t1, x, kb, bps, fps);
   const TileRequests r = tile_requests<STEPS, true>(a, sh, tile);
   const Requests<STEPS, true> rq{a, sh};
   fill_window<STEPS, true>(rq, r, win);
   // publish: the tile's counts, and the counts before each owned request
-  // (s_sync[0] was written before the barriers of the scans above)
+  // (s_sync[0] was written before the barriers of tile_masks' scans)
   const uint32_t tag = (s_sync[0] + 1u) & kTagMask;
   const TileMasks<T::kBlks>& m = sh.m;
   for (int64_t b = r.own_lo + threadIdx.x; b < r.own_hi && b < n; b += kThreads) {
@@ -1205,28 +1209,33 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(88)))
       // the tile's prefix and, when a request spans in, its start counts:
       // from the group's span word when it started in an earlier group, else
       // from its first tile's prefix and its tagged counts there
+      // (all loads issued before any LDS store consumes one: one round trip)
       const int2 pre = get_pair(a.tile_pre + tile);
-      s_go[1] = pre.x;
-      s_go[2] = pre.y;
+      const int64_t j0 = r.spans_in ? rq.off(r.w0) / T::kTile : 0;
+      const bool from_span = j0 < static_cast<int64_t>(k) * kGroupTiles;
+      int2 start = make_int2(0, 0);
+      uint64_t v = 0;
       if (r.spans_in) {
-        const int64_t j0 = rq.off(r.w0) / T::kTile;
-        if (j0 < static_cast<int64_t>(k) * kGroupTiles) {
-          const int2 sp = get_pair(span_word(a, k));
-          s_go[3] = sp.x;
-          s_go[4] = sp.y;
+        if (from_span) {
+          start = get_pair(span_word(a, k));
         } else {
-          const int2 pj = get_pair(a.tile_pre + j0);
-          uint64_t v = 0;
-          for (uint32_t polls = 0;; ++polls) {
-            v = load64(a.req_local + r.w0);
-            if (counts_tag(v) == tag || polls >= kPollLimit) break;
-            __builtin_amdgcn_s_sleep(2);
-          }
-          go = counts_tag(v) == tag;
-          s_go[3] = pj.x + counts_kept(v);
-          s_go[4] = pj.y + counts_moved(v);
+          start = get_pair(a.tile_pre + j0);
+          v = load64(a.req_local + r.w0);
         }
       }
+      if (r.spans_in && !from_span) {
+        for (uint32_t polls = 0; counts_tag(v) != tag && polls < kPollLimit; ++polls) {
+          __builtin_amdgcn_s_sleep(2);
+          v = load64(a.req_local + r.w0);
+        }
+        go = counts_tag(v) == tag;
+        start.x += counts_kept(v);
+        start.y += counts_moved(v);
+      }
+      s_go[1] = pre.x;
+      s_go[2] = pre.y;
+      s_go[3] = start.x;
+      s_go[4] = start.y;
     }
     if (!go) {
       // withdraw: finish_kernel rebuilds this tile's outputs
