@@ -19,9 +19,11 @@
 // Workgroup = (block of R / G query tokens, KV head g, segment), KV head
 // fastest in the grid (workgroup id mod 8 picks the XCD: with 8 KV heads each
 // XCD's L2 serves one head's K/V), with the
-// G q heads of the group packed as rows: row r = token * G + head; R = 256
-// rows at head_dim 64 (4 waves x 64 rows, so each wave's reads of a K/V tile
-// from LDS feed 64 rows), 128 at head_dim 128 (4 waves x 32 rows).  Per
+// G q heads of the group packed as rows: row r = token * G + head; R = 512
+// rows at head_dim 64 (8 waves x 64 rows, so each wave's reads of a K/V tile
+// from LDS feed 64 rows), 256 at head_dim 128 (8 waves x 32 rows); one
+// workgroup per CU, two waves per SIMD, so every K/V tile a CU stages from
+// L2 feeds all of its rows.  Per
 // tile of 128 keys (full layers at head_dim 64) or 64 (K and V key-major in
 // LDS with XOR-swizzled 16 B chunks, double buffered; the next tile's rows
 // stream straight from HBM into LDS with global_load_lds_dwordx4 -- no
@@ -74,8 +76,13 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // 16-row subtiles per wave: 4 at head_dim 64 (each wave's K/V tile reads
 // from LDS feed 64 rows), 2 at head_dim 128 (register budget)
 constexpr int sub_tiles(int d) { return d == 64 ? 4 : 2; }
-constexpr int rows_per_block(int d) { return 4 * 16 * sub_tiles(d); }  // (token, head) rows
-constexpr int kThreads = 256;
+// 8 waves: the register budget allows two waves per SIMD, so a workgroup of
+// 8 fills the CU alone and its K/V tiles feed twice the rows of two 4-wave
+// workgroups (half the tile loads per flop, and twice the math per tile to
+// hide each tile's load behind)
+constexpr int kWaves = 8;
+constexpr int rows_per_block(int d) { return kWaves * 16 * sub_tiles(d); }  // (token, head) rows
+constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.f;  // log2-domain slack before an exact maximum moves
 constexpr float kBig = 4294967296.f;  // 2^32: a weight sum above it is renormalised
@@ -177,7 +184,7 @@ __device__ __forceinline__ int32_t rel_pos(int64_t p, int64_t base) {
 
 // KEYS keys per tile: 128 for full layers at head_dim 64 (half the tile
 // barriers, staging and commits per key), 64 for windowed layers (less of a
-// tile outside the window) and at head_dim 128 (LDS for two workgroups per CU)
+// tile outside the window) and at head_dim 128 (measured faster than 128 there)
 // GEN: the general instance -- logit caps, heads narrower than D (the dims
 // past head_dim zero in the tiles), groups padded to a power of two; the
 // plain instance takes none of these checks.
@@ -302,7 +309,9 @@ __global__ void __launch_bounds__(kThreads, 2) context_attention_kernel(const Ct
   // ^ swz(row) of that key, which it loads.  Each wave fills kBlocksPerWave
   // blocks of K and of V.  Prefix slots are fetched one tile ahead.
   constexpr int kRowsPerBlock = 1024 / (2 * D);
-  constexpr int kBlocksPerWave = kKeys / kRowsPerBlock / 4;
+  constexpr int kBlocksPerWave = kKeys / kRowsPerBlock / kWaves;
+  static_assert(kBlocksPerWave >= 1 && kBlocksPerWave * kRowsPerBlock * kWaves == kKeys, "tile split over waves");
+  static_assert(kThreads >= kKeys, "one thread per key position");
   // slot indices are below 2^32 (a pool of 2^32 slots of one 64-wide bf16
   // head is 512 GiB): int64 indices address rows through their low 32 bits
   uint32_t slot[kBlocksPerWave];

@@ -175,7 +175,7 @@ def test_strided_pool_and_extend_views(device, d, idx_dtype):
 def test_group_sizes(device, d, hq, hkv):
     """GQA groups of 1, 2, 16 and 32 q heads per KV head, and 3 or 1 KV heads
     (the grid's KV head is the workgroup id modulo their count): a block
-    holds rows_per_block / group tokens (256 down to 4), with causal, prefix,
+    holds rows_per_block / group tokens (512 down to 8), with causal, prefix,
     window and sink handling unchanged."""
     c = _case(device, hq, hkv, d, [3, 70, 300], [0, 45, 200], seed=hq + d)
     sinks = (torch.randn(hq, generator=torch.Generator().manual_seed(3))).to(device)
