@@ -38,9 +38,13 @@ Pinned by (``tests/test_oracle_reposition.py``):
 * bitwise V/tail copies, and ``skip_unmapped`` leaving the destination
   untouched.
 
-Parity unpinned: NaN payloads.  A same-position copy here keeps the source
-bits; the reference's fp32 round trip may canonicalise a NaN's payload.  The
-checks use finite inputs only.
+Non-finite inputs follow IEEE-754: infinities propagate through the same
+operations, and a NaN input or an invalid operation (inf - inf, 0 * inf)
+gives a NaN.  A same-position copy keeps the source bits, NaN payloads
+included.  The GPU test ``test_nonfinite_inputs`` holds the kernel to this
+bit for bit wherever the result is not a NaN, and to NaN exactly where this
+restatement has one.  Parity unpinned: the payload of a NaN that the
+rotation produces; each machine's arithmetic picks its own.
 """
 
 import numpy as np

@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 
 def _run_case(device, *, layers=2, heads=2, head_dim=64, rotary_dim=None, kv_dtype=torch.bfloat16,
               table_dtype=torch.float32, neox=True, slots=512, moved=200, seed=0, skip_unmapped=False,
-              same_every=0, misalign=False, slot_stride_extra=0, table_kind="yarn"):
+              same_every=0, misalign=False, slot_stride_extra=0, table_kind="yarn", nonfinite=False):
     rotary_dim = rotary_dim or head_dim
     g = torch.Generator().manual_seed(seed)
     rng = np.random.default_rng(seed)
@@ -35,6 +35,9 @@ def _run_case(device, *, layers=2, heads=2, head_dim=64, rotary_dim=None, kv_dty
         # slot_stride_extra > 0, and a shifted base when misalign is set
         kb = torch.randn((slots * width + 16,), generator=g).to(kv_dtype)
         vb = torch.randn((slots * width + 16,), generator=g).to(kv_dtype)
+        if nonfinite:
+            _plant_nonfinite(kb, rng)
+            _plant_nonfinite(vb, rng)
         kb, vb = kb.to(device), vb.to(device)
         off = 1 if misalign else 0
         k_views.append(kb[off : off + slots * width].view(slots, width)[:, : heads * head_dim].view(slots, heads, head_dim)
@@ -77,10 +80,59 @@ def _run_case(device, *, layers=2, heads=2, head_dim=64, rotary_dim=None, kv_dty
     torch.cuda.synchronize()
     for layer in range(layers):
         got_k, got_v = to_storage(k_views[layer]), to_storage(v_views[layer])
+        if nonfinite:
+            _assert_nan_aware(got_k, k_np[layer], ORACLE_DTYPE[kv_dtype], f"K layer {layer}")
+            # rows whose pair keeps its position are stored as their source
+            # bits, NaN payloads included (context_reposition.py:98-112)
+            same = (pairs[:, 0] == pairs[:, 1]) & (src > 0) & (dst > 0)
+            assert storage_equal(got_k[dst[same]], k_np[layer][dst[same]]), f"K layer {layer}: same-position rows"
+            assert storage_equal(got_v, v_np[layer]), f"V layer {layer}"
+            continue
         if not storage_equal(got_k, k_np[layer]):
             diff = np.argwhere(got_k != k_np[layer])
             raise AssertionError(f"K layer {layer}: {len(diff)} elements differ, first {diff[:5].tolist()}")
         assert storage_equal(got_v, v_np[layer]), f"V layer {layer}"
+
+
+def _plant_nonfinite(buf, rng):
+    """Sets ~3% of a KV buffer to +-inf and NaNs of several payloads (quiet,
+    signalling, negative) in place."""
+    n = buf.numel()
+    idx = torch.from_numpy(rng.choice(n, n // 32, replace=False))
+    if buf.dtype == torch.float32:
+        pats = np.array([0x7F800000, 0xFF800000, 0x7FC00000, 0x7F800001, 0xFFC12345, 0x7FBFFFFF], dtype=np.uint32)
+        bits = torch.from_numpy(pats[rng.integers(0, len(pats), len(idx))].view(np.int32))
+        buf.view(torch.int32)[idx] = bits
+    else:
+        pats = (np.array([0x7F80, 0xFF80, 0x7FC0, 0x7F81, 0xFFC5, 0x7FBF], dtype=np.uint16)
+                if buf.dtype == torch.bfloat16 else
+                np.array([0x7C00, 0xFC00, 0x7E00, 0x7C01, 0xFE05, 0x7DFF], dtype=np.uint16))
+        bits = torch.from_numpy(pats[rng.integers(0, len(pats), len(idx))].view(np.int16))
+        buf.view(torch.int16)[idx] = bits
+
+
+def _assert_nan_aware(got, want, dtype, what):
+    """Bit-exact wherever the oracle's value is not a NaN; a NaN exactly where
+    the oracle has one (the payload of a NaN that the rotation produces is the
+    hardware's: the one part left open)."""
+    from oracle.bf16 import to_f32
+
+    g, w = to_f32(got, dtype), to_f32(want, dtype)
+    gn, wn = np.isnan(g), np.isnan(w)
+    assert np.array_equal(gn, wn), f"{what}: NaN positions differ ({int((gn != wn).sum())} elements)"
+    assert storage_equal(np.asarray(got)[~wn], np.asarray(want)[~wn]), f"{what}: finite or infinite values differ"
+
+
+@pytest.mark.filterwarnings("ignore:invalid value:RuntimeWarning", "ignore:overflow:RuntimeWarning")
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("neox", [True, False])
+def test_nonfinite_inputs(device, kv_dtype, neox):
+    """K and V rows holding +-inf and NaNs (quiet, signalling, negative
+    payloads), with a third of the pairs at their own position: every value
+    the oracle's IEEE arithmetic makes finite or infinite is bit-exact, NaNs
+    land where the oracle's do, V and same-position rows keep their bits."""
+    _run_case(device, kv_dtype=kv_dtype, neox=neox, seed=17, nonfinite=True, same_every=3)
+    _run_case(device, kv_dtype=kv_dtype, neox=neox, rotary_dim=32, seed=18, nonfinite=True, same_every=3)
 
 
 @pytest.mark.parametrize("neox", [True, False])
